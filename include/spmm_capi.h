@@ -1,0 +1,197 @@
+/*
+ * C ABI of the MI355X SpMM engine (libspmm_amd.so).
+ *
+ * The reference exposes a C++ API only (namespace spmm, the src/ headers); this header
+ * is the flat binding an FFI (ctypes, cgo, JNI, N-API) would load.  Each entry
+ * point names the reference declaration it stands for.  The same library also
+ * exports that C++ API itself (the include/spmm/ headers).
+ *
+ * Conventions
+ *   - Plain pointers and sizes only.  spmm_csr_t / spmm_bsr_t have the field
+ *     order and layout of spmm::CSR / spmm::BSR (csr.h:7-14, bsr.h:45-56);
+ *     fp16 data is passed as uint16_t bit patterns.
+ *   - "d_" pointers are device (HBM) pointers, "h_" pointers host pointers.
+ *   - Every function returns SPMM_OK (0) or an error code and never exits the
+ *     process; spmm_c_last_error() gives the message of the calling thread's
+ *     last failure.  (The C++ API keeps the reference's exit/abort behaviour.)
+ *   - stream: a hipStream_t passed as void*; NULL is the null stream, which is
+ *     what the reference launchers use.  Launchers enqueue and return without
+ *     synchronising.
+ *   - Host structs filled by this library (spmm_c_generate_*, *_from_*_host,
+ *     *_read_binary_host) own malloc'd arrays: release them with
+ *     spmm_c_csr_free_host / spmm_c_bsr_free_host.
+ */
+#ifndef SPMM_CAPI_H
+#define SPMM_CAPI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    SPMM_OK          = 0,
+    SPMM_INVALID     = 1, /* bad argument */
+    SPMM_UNSUPPORTED = 2, /* shape contract of the entry point violated */
+    SPMM_HIP_ERROR   = 3, /* HIP runtime error */
+    SPMM_IO_ERROR    = 4, /* file missing or short */
+    SPMM_NO_MEMORY   = 5  /* host allocation failed */
+};
+
+/* Backend ids of spmm_hybrid_plan_t.backend (spmm_hybrid.h:26-29). */
+enum { SPMM_BACKEND_CSR = 0, SPMM_BACKEND_WMMA = 1 };
+
+typedef struct spmm_csr_t {
+    int    num_rows;
+    int    num_cols;
+    int    nnz;
+    int*   row_ptr;
+    int*   col_idx;
+    float* values;
+} spmm_csr_t;
+
+typedef struct spmm_bsr_t {
+    int       num_rows;
+    int       num_cols;
+    int       block_rows;
+    int       block_cols;
+    int       num_blocks;
+    int       nnz;
+    int*      row_ptr;
+    int*      col_idx;
+    uint16_t* values; /* fp16 bits, 256 per block, row-major inside a block */
+} spmm_bsr_t;
+
+typedef struct spmm_bsr_stats_t {
+    int    num_blocks;
+    long   stored_elements;
+    int    original_nnz;
+    double fill_in_ratio;
+    double block_density;
+} spmm_bsr_stats_t;
+
+typedef struct spmm_hybrid_plan_t {
+    int         backend; /* SPMM_BACKEND_* */
+    double      fill_in_ratio;
+    double      block_density;
+    float       threshold;
+    int         n_aligned;
+    const char* reason; /* static string */
+} spmm_hybrid_plan_t;
+
+/* Engine tuning (0 = automatic).  No counterpart in the reference: exposes the
+ * row-block engine's compile-time variants for measurement sweeps. */
+typedef struct spmm_engine_opts_t {
+    int vec;            /* floats per lane per B load: 1, 2, 4 */
+    int waves;          /* waves per workgroup: 4, 8 */
+    int unroll;         /* B rows in flight per wave: 8, 16 */
+    int rows_per_block; /* implicit partition granularity */
+} spmm_engine_opts_t;
+
+const char* spmm_c_last_error(void);
+const char* spmm_c_version(void);
+
+/* ---- host CSR (csr.h:17-39) ------------------------------------------- */
+int spmm_c_csr_alloc_host(int rows, int cols, int nnz, spmm_csr_t* out);   /* csr.h:17 */
+void spmm_c_csr_free_host(spmm_csr_t* m);                                  /* csr.h:18 */
+int spmm_c_csr_from_coo_host(int rows, int cols, int n, const int* row_indices,
+                             const int* col_indices, const float* values,
+                             spmm_csr_t* out);                             /* csr.h:21 */
+int spmm_c_generate_uniform_random_csr(int rows, int cols, float density, int seed,
+                                       spmm_csr_t* out);                   /* csr.h:25 */
+int spmm_c_csr_row_slice_host(const spmm_csr_t* m, int row_begin, int row_end,
+                              spmm_csr_t* out);                            /* csr.h:30 */
+int spmm_c_csr_read_binary_host(const char* path, spmm_csr_t* out);        /* csr.h:34 */
+int spmm_c_csr_write_binary_host(const spmm_csr_t* m, const char* path);   /* csr.h:35 */
+int spmm_c_csr_to_device(const spmm_csr_t* h, spmm_csr_t* d_out);          /* csr.h:38 */
+int spmm_c_csr_free_device(spmm_csr_t* d);                                 /* csr.h:39 */
+
+/* ---- BSR (bsr.h:71-80) ------------------------------------------------ */
+int spmm_c_bsr_from_csr_host(const spmm_csr_t* h, spmm_bsr_t* out);       /* bsr.h:71 */
+void spmm_c_bsr_free_host(spmm_bsr_t* h);                                  /* BSR_host dtor */
+int spmm_c_bsr_to_device(const spmm_bsr_t* h, spmm_bsr_t* d_out);          /* bsr.h:74 */
+int spmm_c_bsr_free_device(spmm_bsr_t* d);                                 /* bsr.h:77 */
+int spmm_c_bsr_compute_stats(const spmm_bsr_t* h, spmm_bsr_stats_t* out);  /* bsr.h:80 */
+
+/* ---- synthetic inputs (harness.cu:114-120, gen_matrices.py:37-81) ----- */
+int spmm_c_generate_dense_row_major(int rows, int cols, int seed, float* h_out);
+int spmm_c_generate_banded_csr(int rows, int cols, int half_bandwidth, int seed,
+                               spmm_csr_t* out);
+int spmm_c_generate_block_diagonal_csr(int rows, int cols, int block, int seed,
+                                       float value_scale, spmm_csr_t* out);
+int spmm_c_generate_power_law_csr(int rows, int cols, double mean_deg, double alpha,
+                                  int max_row_nnz, int seed, spmm_csr_t* out);
+int spmm_c_round_to_fp16(float* h_values, long n); /* values := fp32(fp16_rne(values)) */
+
+/* ---- partition and metrics (spmm_multigpu.cu:26-40, harness.cu:179-201) */
+int spmm_c_nnz_balanced_bounds(const spmm_csr_t* h, int parts, int* h_bounds_out);
+int spmm_c_compare(const float* ours, const float* ref, long n, float* max_abs,
+                   float* max_rel, float* rel_l2);
+int spmm_c_host_reference_f64(const spmm_csr_t* h_A, const float* h_B, int N, int threads,
+                              float* h_C);
+int spmm_c_host_reference_bsr_f32(const spmm_bsr_t* h_A, const float* h_B, int N,
+                                  int threads, float* h_C);
+
+/* ---- kernel entry points (the src/kernels/ headers); d_A is a device CSR -------- */
+int spmm_c_baseline(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
+                    void* stream);                               /* spmm_baseline.h:17  */
+int spmm_c_memopt(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
+                  void* stream);                                 /* spmm_memopt.h:18    */
+int spmm_c_memopt_v2(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
+                     void* stream);                              /* spmm_memopt_v2.h:26 */
+int spmm_c_tiled(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
+                 void* stream);                                  /* spmm_tiled.h:45     */
+int spmm_c_tiled_v2(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
+                    void* stream);                               /* spmm_tiled_v2.h:38  */
+int spmm_c_tiled_v3(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
+                    void* stream);                               /* spmm_tiled_v3.h:40  */
+int spmm_c_tiled_v4(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
+                    void* stream);                               /* spmm_tiled_v4.h:79  */
+/* spmm_tiled_v3 with an explicit nnz-balanced partition: d_bounds holds
+ * parts+1 row bounds (spmm_c_nnz_balanced_bounds); used by spmm_hybrid_run
+ * (spmm_hybrid.cu:103-116 launches spmm_tiled_v3 there). */
+int spmm_c_tiled_v3_partitioned(const spmm_csr_t* d_A, const int* d_bounds, int parts,
+                                const float* d_B, float* d_C, int N, void* stream);
+/* Default number of parts for spmm_c_tiled_v3_partitioned. */
+int spmm_c_default_partition_parts(int num_rows, int nnz);
+/* spmm_tiled_v3 with explicit engine options (no reference counterpart). */
+int spmm_c_tiled_v3_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
+                         const spmm_engine_opts_t* opts, void* stream);
+
+int spmm_c_float_to_half(const float* d_src, uint16_t* d_dst, long n_elements,
+                         void* stream);                          /* spmm_wmma.h:32 */
+int spmm_c_wmma(const spmm_bsr_t* d_bsr, const uint16_t* d_B_fp16, float* d_C, int N,
+                void* stream);                                   /* spmm_wmma.h:39 */
+
+/* ---- hybrid dispatch (spmm_hybrid.h:48-64) ---------------------------- */
+float spmm_c_hybrid_default_threshold(void);
+int spmm_c_hybrid_choose(const spmm_csr_t* h_A, int N, float fill_in_threshold,
+                         spmm_hybrid_plan_t* out);               /* spmm_hybrid.h:48 */
+const char* spmm_c_backend_name(int backend);                    /* spmm_hybrid.h:51 */
+int spmm_c_hybrid_run(const spmm_hybrid_plan_t* plan, const spmm_csr_t* h_A,
+                      const float* h_B, float* h_C, int N, int warmup, int iters,
+                      float* ms_out);                            /* spmm_hybrid.h:62 */
+
+/* ---- measurement helpers (no reference counterpart) -------------------
+ * Launch one entry point `reps` times back to back on `stream` without
+ * synchronising, so a caller's events can bracket a batch.  kernel ids:
+ * 0 baseline, 1 memopt, 2 memopt_v2, 3 tiled, 4 tiled_v2, 5 tiled_v3,
+ * 6 tiled_v4 (d_A_any is a spmm_csr_t*), 7 wmma (d_A_any is a spmm_bsr_t*,
+ * d_B a uint16_t* of fp16 bits). */
+int spmm_c_launch_repeat(int kernel_id, const void* d_A_any, const void* d_B, float* d_C,
+                         int N, int reps, void* stream);
+/* Same with explicit engine options for kernel id 5 (tiled_v3). */
+int spmm_c_launch_repeat_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
+                              const spmm_engine_opts_t* opts, int reps, void* stream);
+/* Times `reps` back-to-back launches between two hipEvents recorded on
+ * `stream`; writes the elapsed milliseconds of the whole batch. */
+int spmm_c_time_repeat(int kernel_id, const void* d_A_any, const void* d_B, float* d_C,
+                       int N, int reps, void* stream, float* ms_out);
+int spmm_c_device_synchronize(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPMM_CAPI_H */

@@ -1,0 +1,232 @@
+// BSR (16x16 fp16 blocks) x dense fp16 B on gfx950 matrix cores, and the
+// fp32 -> fp16 conversion (roles of spmm_wmma and float_to_half,
+// spmm_wmma.cu:18-23 and :49-117).
+//
+// MFMA operand layout used (v_mfma_f32_16x16x32_f16, wave64, lane = 16*g + t):
+//   A operand: lane holds A[t][kmap(g, 0..7)]       (8 fp16)
+//   B operand: lane holds B[kmap(g, 0..7)][t]       (8 fp16)
+//   D        : lane holds D[4*g + i][t], i = 0..3   (4 fp32)
+// kmap(g, i) = 8*g + i.  The contraction only needs A and B to use the same
+// kmap, so blocks pair up as: g = 0,1 -> block b (its columns 8*g .. 8*g+7),
+// g = 2,3 -> block b+1.
+//
+// B is K-contiguous in the operand but N-contiguous in memory, so each wave
+// stages the 32 B rows of a block pair (its 16*J columns) in LDS with plain
+// 16-byte row loads and reads the operand back column-wise.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "engine.h"
+#include "spmm/utils.h"
+
+namespace spmm {
+namespace engine {
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float    f32x4 __attribute__((ext_vector_type(4)));
+
+// fp32 -> fp16 (round to nearest even), 8 elements per lane on the aligned body.
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict__ src,
+                                                         _Float16* __restrict__ dst, long n,
+                                                         int vector_ok) {
+    const long tid = static_cast<long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (vector_ok) {
+        const long i = tid * 8;
+        if (i + 8 <= n) {
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(src + i);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(src + i + 4);
+            f16x8 h;
+            h[0] = static_cast<_Float16>(lo[0]);
+            h[1] = static_cast<_Float16>(lo[1]);
+            h[2] = static_cast<_Float16>(lo[2]);
+            h[3] = static_cast<_Float16>(lo[3]);
+            h[4] = static_cast<_Float16>(hi[0]);
+            h[5] = static_cast<_Float16>(hi[1]);
+            h[6] = static_cast<_Float16>(hi[2]);
+            h[7] = static_cast<_Float16>(hi[3]);
+            *reinterpret_cast<f16x8*>(dst + i) = h;
+        } else {
+            for (long e = i; e < n; ++e) dst[e] = static_cast<_Float16>(src[e]);
+        }
+    } else if (tid < n) {
+        dst[tid] = static_cast<_Float16>(src[tid]);
+    }
+}
+
+struct BsrArgs {
+    const int*      row_ptr;
+    const int*      col_idx;
+    const _Float16* vals;
+    const _Float16* B;
+    float*          C;
+    int             M;
+    int             K;
+    int             N;
+    int             block_rows;
+    int             b_vec_ok;  // N % 8 == 0 and B 16-byte aligned
+};
+
+// One wave = one block-row x (16*J) columns.  Workgroup = 4 independent waves
+// on 4 consecutive block-rows (same column tile).
+template <int J>
+__global__ __launch_bounds__(256) void bsr_mfma_kernel(BsrArgs a) {
+    constexpr int WN     = 16 * J;   // columns per wave
+    constexpr int STRIDE = WN + 2;   // LDS row stride in fp16 (pad against bank conflicts)
+    constexpr int CHUNKS = WN / 8;   // 16-byte chunks per staged row
+    __shared__ _Float16 s_b[4][32 * STRIDE];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g    = lane >> 4;
+    const int t    = lane & 15;
+    const int br   = blockIdx.x * 4 + wave;
+    const int n0   = blockIdx.y * WN;
+    if (br >= a.block_rows) return;  // no workgroup barrier below: waves are independent
+    _Float16* sb = s_b[wave];
+
+    f32x4 acc[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) acc[j] = f32x4(0.0f);
+
+    const int b_begin = a.row_ptr[br];
+    const int b_end   = a.row_ptr[br + 1];
+    for (int b = b_begin; b < b_end; b += 2) {
+        const bool pair = (b + 1) < b_end;
+        const int  bc0  = a.col_idx[b];
+        const int  bc1  = pair ? a.col_idx[b + 1] : 0;
+
+        // A operand: row t of block (g < 2 ? b : b+1), columns 8*(g&1) .. +7.
+        f16x8 af = f16x8(static_cast<_Float16>(0.0f));
+        if (g < 2 || pair) {
+            const int blk = g < 2 ? b : b + 1;
+            af = *reinterpret_cast<const f16x8*>(a.vals + static_cast<size_t>(blk) * 256 +
+                                                 t * 16 + 8 * (g & 1));
+        }
+
+        // Stage B rows: staged row s < 16 is K-row bc0*16 + s, s >= 16 is bc1*16 + s-16.
+        for (int idx = lane; idx < 32 * CHUNKS; idx += 64) {
+            const int s  = idx / CHUNKS;
+            const int ch = idx % CHUNKS;
+            const int k  = s < 16 ? bc0 * 16 + s : bc1 * 16 + (s - 16);
+            const int n  = n0 + ch * 8;
+            const bool row_ok = (s < 16 || pair) && static_cast<unsigned>(k) < static_cast<unsigned>(a.K);
+            f16x8 v = f16x8(static_cast<_Float16>(0.0f));
+            if (row_ok) {
+                const _Float16* src = a.B + static_cast<size_t>(k) * a.N + n;
+                if (a.b_vec_ok && n + 8 <= a.N) {
+                    v = *reinterpret_cast<const f16x8*>(src);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        if (n + e < a.N) v[e] = src[e];
+                    }
+                }
+            }
+            f16x2* dst = reinterpret_cast<f16x2*>(sb + s * STRIDE + ch * 8);
+            dst[0] = f16x2{v[0], v[1]};
+            dst[1] = f16x2{v[2], v[3]};
+            dst[2] = f16x2{v[4], v[5]};
+            dst[3] = f16x2{v[6], v[7]};
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+        __builtin_amdgcn_wave_barrier();
+
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            f16x8 bf;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) bf[i] = sb[(8 * g + i) * STRIDE + 16 * j + t];
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j], 0, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next pair overwrites
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // D layout: lane holds rows 4*g + i, column t of each 16-column tile.
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int col = n0 + 16 * j + t;
+        if (col >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = br * 16 + 4 * g + i;
+            if (row < a.M) a.C[static_cast<size_t>(row) * a.N + col] = acc[j][i];
+        }
+    }
+}
+
+Error fail(int status, std::string msg) { return Error{status, std::move(msg)}; }
+
+Error from_hip(hipError_t e, const char* what) {
+    if (e == hipSuccess) return Error{};
+    return fail(kHipError, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <int J>
+hipError_t run_bsr(const BsrArgs& args, hipStream_t stream) {
+    dim3 grid(ceil_div(args.block_rows, 4), ceil_div(args.N, 16 * J));
+    hipLaunchKernelGGL((bsr_mfma_kernel<J>), grid, dim3(256), 0, stream, args);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+Error launch_float_to_half(const float* src, half* dst, long n, hipStream_t stream) {
+    if (n < 0) return fail(kInvalid, "negative element count");
+    if (n == 0) return Error{};
+    if (src == nullptr || dst == nullptr) return fail(kInvalid, "null device pointer");
+    const bool vec = (reinterpret_cast<uintptr_t>(src) % 16 == 0) &&
+                     (reinterpret_cast<uintptr_t>(dst) % 16 == 0);
+    const long threads = vec ? (n + 7) / 8 : n;
+    const long blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffffL) return fail(kInvalid, "element count too large");
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                       stream, src, reinterpret_cast<_Float16*>(dst), n, vec ? 1 : 0);
+    return from_hip(hipGetLastError(), "float_to_half launch");
+}
+
+Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t stream) {
+    if (A.num_rows < 0 || A.num_cols < 0 || A.num_blocks < 0 || N < 0) {
+        return fail(kInvalid, "negative matrix dimension");
+    }
+    if (A.block_rows != (A.num_rows + 15) / 16 || A.block_cols != (A.num_cols + 15) / 16) {
+        return fail(kInvalid, "BSR block dimensions do not match num_rows / num_cols");
+    }
+    if (A.num_rows == 0 || N == 0) return Error{};
+    if (A.row_ptr == nullptr || C == nullptr || B == nullptr) {
+        return fail(kInvalid, "null device pointer");
+    }
+    if (A.num_blocks > 0 && (A.col_idx == nullptr || A.values == nullptr)) {
+        return fail(kInvalid, "null device pointer");
+    }
+    if (reinterpret_cast<uintptr_t>(A.values) % 16 != 0) {
+        return fail(kInvalid, "BSR values must be 16-byte aligned");
+    }
+    BsrArgs args{A.row_ptr,
+                 A.col_idx,
+                 reinterpret_cast<const _Float16*>(A.values),
+                 reinterpret_cast<const _Float16*>(B),
+                 C,
+                 A.num_rows,
+                 A.num_cols,
+                 N,
+                 A.block_rows,
+                 (N % 8 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0) ? 1 : 0};
+    hipError_t e;
+    if (N <= 16) {
+        e = run_bsr<1>(args, stream);
+    } else if (N <= 32) {
+        e = run_bsr<2>(args, stream);
+    } else {
+        e = run_bsr<4>(args, stream);
+    }
+    return from_hip(e, "spmm_wmma launch");
+}
+
+}  // namespace engine
+}  // namespace spmm

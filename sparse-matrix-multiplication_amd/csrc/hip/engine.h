@@ -1,0 +1,63 @@
+#pragma once
+// Internal launch layer shared by the C++ drop-in API, the C ABI and the
+// hybrid dispatcher.  Every launcher validates its arguments, enqueues on the
+// given stream and returns a status; the public wrappers turn a status into
+// the reference's conventions (exit / abort) or into a C error code.
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "spmm/bsr.h"
+#include "spmm/csr.h"
+
+namespace spmm {
+namespace engine {
+
+enum Status : int {
+    kOk          = 0,
+    kInvalid     = 1,  // bad argument (negative size, null pointer, misaligned)
+    kUnsupported = 2,  // a shape contract of the entry point is violated
+    kHipError    = 3,  // the HIP runtime reported an error
+};
+
+// Which reference entry point is being served.
+enum class CsrRole : int {
+    Baseline = 0,
+    Memopt   = 1,
+    MemoptV2 = 2,
+    Tiled    = 3,
+    TiledV2  = 4,
+    TiledV3  = 5,
+    TiledV4  = 6,
+};
+
+// Tuning of the row-block engine.  Zero fields mean "choose automatically".
+struct EngineOpts {
+    int vec            = 0;  // floats per lane per B load: 1, 2 or 4
+    int waves          = 0;  // waves per workgroup: 4 or 8
+    int unroll         = 0;  // B-row loads in flight per wave: 8 or 16
+    int rows_per_block = 0;  // implicit partition: rows per workgroup
+};
+
+struct Error {
+    int         status = kOk;
+    std::string message;
+};
+
+// d_bounds (nullable) is a device array of parts+1 row bounds produced by
+// nnz_balanced_bounds; when given, workgroup g owns rows [bounds[g], bounds[g+1]).
+Error launch_csr(CsrRole role, const CSR& d_A, const float* d_B, float* d_C, int N,
+                 hipStream_t stream, const int* d_bounds = nullptr, int parts = 0,
+                 const EngineOpts* opts = nullptr);
+
+Error launch_float_to_half(const float* d_src, half* d_dst, long n, hipStream_t stream);
+
+Error launch_bsr(const BSR& d_A, const half* d_B, float* d_C, int N, hipStream_t stream);
+
+// Number of workgroups the engine uses for an explicit partition of this CSR.
+int default_partition_parts(int num_rows, int nnz);
+
+}  // namespace engine
+}  // namespace spmm

@@ -1,0 +1,538 @@
+"""Python binding of the MI355X SpMM engine (ctypes over include/spmm_capi.h).
+
+Mirrors the reference's C++ API for the hot path (reference src/csr.h,
+src/bsr.h, src/kernels/*.h, src/spmm_hybrid.h): the same names, argument
+meaning and failure conditions, raised as ``SpmmError`` instead of exiting.
+
+Device buffers are torch tensors on ``cuda`` (torch is only the allocator and
+the stream handle); every launch goes through ``libspmm_amd.so``.  When the
+library is missing this module raises on first use -- there is no CPU
+fallback for any device entry point.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "build", "libspmm_amd.so")
+
+SPMM_OK, SPMM_INVALID, SPMM_UNSUPPORTED, SPMM_HIP_ERROR, SPMM_IO_ERROR, SPMM_NO_MEMORY = range(6)
+BACKEND_CSR, BACKEND_WMMA = 0, 1
+
+# kernel ids of spmm_c_launch_repeat / spmm_c_time_repeat
+KERNEL_IDS = {
+    "baseline": 0, "memopt": 1, "memopt_v2": 2, "tiled": 3,
+    "tiled_v2": 4, "tiled_v3": 5, "tiled_v4": 6, "wmma": 7,
+}
+CSR_KERNELS = ("baseline", "memopt", "memopt_v2", "tiled", "tiled_v2", "tiled_v3", "tiled_v4")
+
+
+class SpmmError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+
+
+class CsrT(ctypes.Structure):
+    _fields_ = [("num_rows", ctypes.c_int), ("num_cols", ctypes.c_int), ("nnz", ctypes.c_int),
+                ("row_ptr", ctypes.c_void_p), ("col_idx", ctypes.c_void_p),
+                ("values", ctypes.c_void_p)]
+
+
+class BsrT(ctypes.Structure):
+    _fields_ = [("num_rows", ctypes.c_int), ("num_cols", ctypes.c_int),
+                ("block_rows", ctypes.c_int), ("block_cols", ctypes.c_int),
+                ("num_blocks", ctypes.c_int), ("nnz", ctypes.c_int),
+                ("row_ptr", ctypes.c_void_p), ("col_idx", ctypes.c_void_p),
+                ("values", ctypes.c_void_p)]
+
+
+class BsrStatsT(ctypes.Structure):
+    _fields_ = [("num_blocks", ctypes.c_int), ("stored_elements", ctypes.c_long),
+                ("original_nnz", ctypes.c_int), ("fill_in_ratio", ctypes.c_double),
+                ("block_density", ctypes.c_double)]
+
+
+class HybridPlanT(ctypes.Structure):
+    _fields_ = [("backend", ctypes.c_int), ("fill_in_ratio", ctypes.c_double),
+                ("block_density", ctypes.c_double), ("threshold", ctypes.c_float),
+                ("n_aligned", ctypes.c_int), ("reason", ctypes.c_char_p)]
+
+
+class EngineOptsT(ctypes.Structure):
+    _fields_ = [("vec", ctypes.c_int), ("waves", ctypes.c_int), ("unroll", ctypes.c_int),
+                ("rows_per_block", ctypes.c_int)]
+
+
+_P = ctypes.POINTER
+_vp, _int, _long, _float, _double = (ctypes.c_void_p, ctypes.c_int, ctypes.c_long,
+                                     ctypes.c_float, ctypes.c_double)
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "spmm_c_last_error": (ctypes.c_char_p, []),
+    "spmm_c_version": (ctypes.c_char_p, []),
+    "spmm_c_csr_alloc_host": (_int, [_int, _int, _int, _P(CsrT)]),
+    "spmm_c_csr_free_host": (None, [_P(CsrT)]),
+    "spmm_c_csr_from_coo_host": (_int, [_int, _int, _int, _vp, _vp, _vp, _P(CsrT)]),
+    "spmm_c_generate_uniform_random_csr": (_int, [_int, _int, _float, _int, _P(CsrT)]),
+    "spmm_c_csr_row_slice_host": (_int, [_P(CsrT), _int, _int, _P(CsrT)]),
+    "spmm_c_csr_read_binary_host": (_int, [ctypes.c_char_p, _P(CsrT)]),
+    "spmm_c_csr_write_binary_host": (_int, [_P(CsrT), ctypes.c_char_p]),
+    "spmm_c_csr_to_device": (_int, [_P(CsrT), _P(CsrT)]),
+    "spmm_c_csr_free_device": (_int, [_P(CsrT)]),
+    "spmm_c_bsr_from_csr_host": (_int, [_P(CsrT), _P(BsrT)]),
+    "spmm_c_bsr_free_host": (None, [_P(BsrT)]),
+    "spmm_c_bsr_to_device": (_int, [_P(BsrT), _P(BsrT)]),
+    "spmm_c_bsr_free_device": (_int, [_P(BsrT)]),
+    "spmm_c_bsr_compute_stats": (_int, [_P(BsrT), _P(BsrStatsT)]),
+    "spmm_c_generate_dense_row_major": (_int, [_int, _int, _int, _vp]),
+    "spmm_c_generate_banded_csr": (_int, [_int, _int, _int, _int, _P(CsrT)]),
+    "spmm_c_generate_block_diagonal_csr": (_int, [_int, _int, _int, _int, _float, _P(CsrT)]),
+    "spmm_c_generate_power_law_csr": (_int, [_int, _int, _double, _double, _int, _int, _P(CsrT)]),
+    "spmm_c_round_to_fp16": (_int, [_vp, _long]),
+    "spmm_c_nnz_balanced_bounds": (_int, [_P(CsrT), _int, _vp]),
+    "spmm_c_compare": (_int, [_vp, _vp, _long, _P(_float), _P(_float), _P(_float)]),
+    "spmm_c_host_reference_f64": (_int, [_P(CsrT), _vp, _int, _int, _vp]),
+    "spmm_c_host_reference_bsr_f32": (_int, [_P(BsrT), _vp, _int, _int, _vp]),
+    "spmm_c_baseline": (_int, [_P(CsrT), _vp, _vp, _int, _vp]),
+    "spmm_c_memopt": (_int, [_P(CsrT), _vp, _vp, _int, _vp]),
+    "spmm_c_memopt_v2": (_int, [_P(CsrT), _vp, _vp, _int, _vp]),
+    "spmm_c_tiled": (_int, [_P(CsrT), _vp, _vp, _int, _vp]),
+    "spmm_c_tiled_v2": (_int, [_P(CsrT), _vp, _vp, _int, _vp]),
+    "spmm_c_tiled_v3": (_int, [_P(CsrT), _vp, _vp, _int, _vp]),
+    "spmm_c_tiled_v4": (_int, [_P(CsrT), _vp, _vp, _int, _vp]),
+    "spmm_c_tiled_v3_partitioned": (_int, [_P(CsrT), _vp, _int, _vp, _vp, _int, _vp]),
+    "spmm_c_default_partition_parts": (_int, [_int, _int]),
+    "spmm_c_tiled_v3_opts": (_int, [_P(CsrT), _vp, _vp, _int, _P(EngineOptsT), _vp]),
+    "spmm_c_float_to_half": (_int, [_vp, _vp, _long, _vp]),
+    "spmm_c_wmma": (_int, [_P(BsrT), _vp, _vp, _int, _vp]),
+    "spmm_c_hybrid_default_threshold": (_float, []),
+    "spmm_c_hybrid_choose": (_int, [_P(CsrT), _int, _float, _P(HybridPlanT)]),
+    "spmm_c_backend_name": (ctypes.c_char_p, [_int]),
+    "spmm_c_hybrid_run": (_int, [_P(HybridPlanT), _P(CsrT), _vp, _vp, _int, _int, _int, _P(_float)]),
+    "spmm_c_launch_repeat": (_int, [_int, _vp, _vp, _vp, _int, _int, _vp]),
+    "spmm_c_launch_repeat_opts": (_int, [_P(CsrT), _vp, _vp, _int, _P(EngineOptsT), _int, _vp]),
+    "spmm_c_time_repeat": (_int, [_int, _vp, _vp, _vp, _int, _int, _vp, _P(_float)]),
+    "spmm_c_device_synchronize": (_int, []),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    """Load libspmm_amd.so (built by ``make -C sparse-matrix-multiplication_amd``)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise SpmmError(SPMM_INVALID, f"{LIB_PATH} is not built; run "
+                            "`make -C sparse-matrix-multiplication_amd` (or __graft_entry__.build())")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != SPMM_OK:
+        raise SpmmError(rc, lib().spmm_c_last_error().decode())
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data if a.size else 0
+
+
+# ---------------------------------------------------------------------------
+# Host CSR / BSR (copies out of the library's malloc'd arrays)
+# ---------------------------------------------------------------------------
+@dataclass
+class HostCSR:
+    """Host CSR (spmm::CSR, reference csr.h:7-14) held as numpy arrays."""
+    num_rows: int
+    num_cols: int
+    row_ptr: np.ndarray  # int32[num_rows + 1]
+    col_idx: np.ndarray  # int32[nnz]
+    values: np.ndarray   # float32[nnz]
+
+    @property
+    def nnz(self) -> int:
+        return int(self.col_idx.size)
+
+    def struct(self) -> CsrT:
+        self.row_ptr = np.ascontiguousarray(self.row_ptr, dtype=np.int32)
+        self.col_idx = np.ascontiguousarray(self.col_idx, dtype=np.int32)
+        self.values = np.ascontiguousarray(self.values, dtype=np.float32)
+        return CsrT(self.num_rows, self.num_cols, self.nnz, _ptr(self.row_ptr),
+                    _ptr(self.col_idx), _ptr(self.values))
+
+    def to_dense(self) -> np.ndarray:
+        d = np.zeros((self.num_rows, self.num_cols), dtype=np.float64)
+        rows = np.repeat(np.arange(self.num_rows), np.diff(self.row_ptr))
+        np.add.at(d, (rows, self.col_idx), self.values.astype(np.float64))
+        return d
+
+
+@dataclass
+class HostBSR:
+    """Host BSR (spmm::BSR_host, reference bsr.h:25-42); values are fp16 bits."""
+    num_rows: int
+    num_cols: int
+    block_rows: int
+    block_cols: int
+    nnz: int
+    row_ptr: np.ndarray   # int32[block_rows + 1]
+    col_idx: np.ndarray   # int32[num_blocks]
+    values: np.ndarray    # uint16[num_blocks * 256]
+
+    @property
+    def num_blocks(self) -> int:
+        return int(self.col_idx.size)
+
+    def struct(self) -> BsrT:
+        self.row_ptr = np.ascontiguousarray(self.row_ptr, dtype=np.int32)
+        self.col_idx = np.ascontiguousarray(self.col_idx, dtype=np.int32)
+        self.values = np.ascontiguousarray(self.values, dtype=np.uint16)
+        return BsrT(self.num_rows, self.num_cols, self.block_rows, self.block_cols,
+                    self.num_blocks, self.nnz, _ptr(self.row_ptr), _ptr(self.col_idx),
+                    _ptr(self.values))
+
+
+def _csr_from_struct(s: CsrT) -> HostCSR:
+    """Copy a library-owned host CSR into numpy and free the library copy."""
+    try:
+        rp = np.ctypeslib.as_array(ctypes.cast(s.row_ptr, _P(ctypes.c_int32)),
+                                   (s.num_rows + 1,)).copy()
+        ci = (np.ctypeslib.as_array(ctypes.cast(s.col_idx, _P(ctypes.c_int32)), (s.nnz,)).copy()
+              if s.nnz else np.zeros(0, np.int32))
+        va = (np.ctypeslib.as_array(ctypes.cast(s.values, _P(ctypes.c_float)), (s.nnz,)).copy()
+              if s.nnz else np.zeros(0, np.float32))
+        return HostCSR(s.num_rows, s.num_cols, rp, ci, va)
+    finally:
+        lib().spmm_c_csr_free_host(ctypes.byref(s))
+
+
+def _bsr_from_struct(s: BsrT) -> HostBSR:
+    try:
+        rp = np.ctypeslib.as_array(ctypes.cast(s.row_ptr, _P(ctypes.c_int32)),
+                                   (s.block_rows + 1,)).copy()
+        ci = (np.ctypeslib.as_array(ctypes.cast(s.col_idx, _P(ctypes.c_int32)),
+                                    (s.num_blocks,)).copy()
+              if s.num_blocks else np.zeros(0, np.int32))
+        va = (np.ctypeslib.as_array(ctypes.cast(s.values, _P(ctypes.c_uint16)),
+                                    (s.num_blocks * 256,)).copy()
+              if s.num_blocks else np.zeros(0, np.uint16))
+        return HostBSR(s.num_rows, s.num_cols, s.block_rows, s.block_cols, s.nnz, rp, ci, va)
+    finally:
+        lib().spmm_c_bsr_free_host(ctypes.byref(s))
+
+
+def generate_uniform_random_csr(rows: int, cols: int, density: float, seed: int) -> HostCSR:
+    """Reference csr.cu:74-103."""
+    s = CsrT()
+    _check(lib().spmm_c_generate_uniform_random_csr(rows, cols, density, seed, ctypes.byref(s)))
+    return _csr_from_struct(s)
+
+
+def generate_banded_csr(rows: int, cols: int, half_bandwidth: int, seed: int) -> HostCSR:
+    s = CsrT()
+    _check(lib().spmm_c_generate_banded_csr(rows, cols, half_bandwidth, seed, ctypes.byref(s)))
+    return _csr_from_struct(s)
+
+
+def generate_block_diagonal_csr(rows: int, cols: int, block: int, seed: int,
+                                value_scale: float = 0.1) -> HostCSR:
+    s = CsrT()
+    _check(lib().spmm_c_generate_block_diagonal_csr(rows, cols, block, seed, value_scale,
+                                                    ctypes.byref(s)))
+    return _csr_from_struct(s)
+
+
+def generate_power_law_csr(rows: int, cols: int, mean_deg: float, alpha: float,
+                           max_row_nnz: int, seed: int) -> HostCSR:
+    s = CsrT()
+    _check(lib().spmm_c_generate_power_law_csr(rows, cols, mean_deg, alpha, max_row_nnz, seed,
+                                               ctypes.byref(s)))
+    return _csr_from_struct(s)
+
+
+def generate_dense_row_major(rows: int, cols: int, seed: int) -> np.ndarray:
+    """Reference harness.cu:114-120."""
+    out = np.empty((rows, cols), dtype=np.float32)
+    _check(lib().spmm_c_generate_dense_row_major(rows, cols, seed, _ptr(out)))
+    return out
+
+
+def round_to_fp16(a: np.ndarray) -> np.ndarray:
+    out = np.ascontiguousarray(a, dtype=np.float32).copy()
+    _check(lib().spmm_c_round_to_fp16(_ptr(out), out.size))
+    return out
+
+
+def csr_from_coo_host(rows: int, cols: int, r, c, v) -> HostCSR:
+    """Reference csr.cu:44-72."""
+    r = np.ascontiguousarray(r, dtype=np.int32)
+    c = np.ascontiguousarray(c, dtype=np.int32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    if not (r.size == c.size == v.size):
+        raise SpmmError(SPMM_INVALID, "csr_from_coo_host: triplet size mismatch")
+    n = int(v.size)
+    s = CsrT()
+    _check(lib().spmm_c_csr_from_coo_host(rows, cols, n, _ptr(r), _ptr(c), _ptr(v),
+                                          ctypes.byref(s)))
+    return _csr_from_struct(s)
+
+
+def csr_row_slice_host(m: HostCSR, row_begin: int, row_end: int) -> HostCSR:
+    s = CsrT()
+    src = m.struct()
+    _check(lib().spmm_c_csr_row_slice_host(ctypes.byref(src), row_begin, row_end, ctypes.byref(s)))
+    return _csr_from_struct(s)
+
+
+def csr_read_binary_host(path: str) -> HostCSR:
+    s = CsrT()
+    _check(lib().spmm_c_csr_read_binary_host(os.fsencode(path), ctypes.byref(s)))
+    return _csr_from_struct(s)
+
+
+def csr_write_binary_host(m: HostCSR, path: str) -> None:
+    src = m.struct()
+    _check(lib().spmm_c_csr_write_binary_host(ctypes.byref(src), os.fsencode(path)))
+
+
+def bsr_from_csr_host(m: HostCSR) -> HostBSR:
+    """Reference bsr.cu:30-109."""
+    s = BsrT()
+    src = m.struct()
+    _check(lib().spmm_c_bsr_from_csr_host(ctypes.byref(src), ctypes.byref(s)))
+    return _bsr_from_struct(s)
+
+
+def bsr_compute_stats(b: HostBSR) -> BsrStatsT:
+    st = BsrStatsT()
+    src = b.struct()
+    _check(lib().spmm_c_bsr_compute_stats(ctypes.byref(src), ctypes.byref(st)))
+    return st
+
+
+def nnz_balanced_bounds(m: HostCSR, parts: int) -> np.ndarray:
+    out = np.empty(parts + 1, dtype=np.int32)
+    src = m.struct()
+    _check(lib().spmm_c_nnz_balanced_bounds(ctypes.byref(src), parts, _ptr(out)))
+    return out
+
+
+def default_partition_parts(num_rows: int, nnz: int) -> int:
+    return int(lib().spmm_c_default_partition_parts(num_rows, nnz))
+
+
+def compare(ours: np.ndarray, ref: np.ndarray):
+    """Reference harness.cu:179-196 -> (max_abs, max_rel, rel_l2)."""
+    a = np.ascontiguousarray(ours, dtype=np.float32).ravel()
+    b = np.ascontiguousarray(ref, dtype=np.float32).ravel()
+    ma, mr, rl = ctypes.c_float(), ctypes.c_float(), ctypes.c_float()
+    _check(lib().spmm_c_compare(_ptr(a), _ptr(b), a.size, ctypes.byref(ma), ctypes.byref(mr),
+                                ctypes.byref(rl)))
+    return ma.value, mr.value, rl.value
+
+
+def host_reference_f64(m: HostCSR, B: np.ndarray, threads: int = 0) -> np.ndarray:
+    B = np.ascontiguousarray(B, dtype=np.float32)
+    N = B.shape[1]
+    out = np.empty((m.num_rows, N), dtype=np.float32)
+    src = m.struct()
+    _check(lib().spmm_c_host_reference_f64(ctypes.byref(src), _ptr(B), N, threads, _ptr(out)))
+    return out
+
+
+@dataclass
+class Plan:
+    backend: int
+    fill_in_ratio: float
+    block_density: float
+    threshold: float
+    n_aligned: bool
+    reason: str
+
+    @property
+    def backend_name(self) -> str:
+        return lib().spmm_c_backend_name(self.backend).decode()
+
+
+def hybrid_default_threshold() -> float:
+    return float(lib().spmm_c_hybrid_default_threshold())
+
+
+def hybrid_choose(m: HostCSR, N: int, threshold: Optional[float] = None) -> Plan:
+    """Reference spmm_hybrid.cu:32-56."""
+    if threshold is None:
+        threshold = hybrid_default_threshold()
+    p = HybridPlanT()
+    src = m.struct()
+    _check(lib().spmm_c_hybrid_choose(ctypes.byref(src), N, threshold, ctypes.byref(p)))
+    return Plan(p.backend, p.fill_in_ratio, p.block_density, p.threshold, bool(p.n_aligned),
+                p.reason.decode())
+
+
+def backend_name(backend: int) -> str:
+    return lib().spmm_c_backend_name(backend).decode()
+
+
+def hybrid_run(plan: Plan, m: HostCSR, B: np.ndarray, warmup: int = 3, iters: int = 10):
+    """Reference spmm_hybrid.cu:58-125: host in, host out -> (C, median ms)."""
+    B = np.ascontiguousarray(B, dtype=np.float32)
+    N = B.shape[1]
+    C = np.empty((m.num_rows, N), dtype=np.float32)
+    p = HybridPlanT(plan.backend, plan.fill_in_ratio, plan.block_density, plan.threshold,
+                    int(plan.n_aligned), plan.reason.encode())
+    ms = ctypes.c_float()
+    src = m.struct()
+    _check(lib().spmm_c_hybrid_run(ctypes.byref(p), ctypes.byref(src), _ptr(B), _ptr(C), N,
+                                   warmup, iters, ctypes.byref(ms)))
+    return C, ms.value
+
+
+# ---------------------------------------------------------------------------
+# Device side (torch tensors as HBM buffers)
+# ---------------------------------------------------------------------------
+def _torch():
+    import torch  # imported lazily: host-only users never need it
+    return torch
+
+
+def _stream_handle(stream=None) -> int:
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return int(s.cuda_stream)
+
+
+class DeviceCSR:
+    """Device CSR whose three arrays are torch tensors (spmm::CSR with HBM pointers)."""
+
+    def __init__(self, host: HostCSR, device: str = "cuda"):
+        torch = _torch()
+        self.num_rows, self.num_cols, self.nnz = host.num_rows, host.num_cols, host.nnz
+        self.row_ptr = torch.from_numpy(np.ascontiguousarray(host.row_ptr, np.int32)).to(device)
+        self.col_idx = torch.from_numpy(np.ascontiguousarray(host.col_idx, np.int32)).to(device)
+        self.values = torch.from_numpy(np.ascontiguousarray(host.values, np.float32)).to(device)
+
+    def struct(self) -> CsrT:
+        return CsrT(self.num_rows, self.num_cols, self.nnz, self.row_ptr.data_ptr(),
+                    self.col_idx.data_ptr() if self.nnz else 0,
+                    self.values.data_ptr() if self.nnz else 0)
+
+
+class DeviceBSR:
+    """Device BSR (spmm::BSR): fp16 blocks as an int16 torch tensor of bit patterns."""
+
+    def __init__(self, host: HostBSR, device: str = "cuda"):
+        torch = _torch()
+        self.num_rows, self.num_cols = host.num_rows, host.num_cols
+        self.block_rows, self.block_cols = host.block_rows, host.block_cols
+        self.num_blocks, self.nnz = host.num_blocks, host.nnz
+        self.row_ptr = torch.from_numpy(np.ascontiguousarray(host.row_ptr, np.int32)).to(device)
+        self.col_idx = torch.from_numpy(np.ascontiguousarray(host.col_idx, np.int32)).to(device)
+        self.values = torch.from_numpy(
+            np.ascontiguousarray(host.values, np.uint16).view(np.int16)).to(device)
+
+    def struct(self) -> BsrT:
+        return BsrT(self.num_rows, self.num_cols, self.block_rows, self.block_cols,
+                    self.num_blocks, self.nnz, self.row_ptr.data_ptr(),
+                    self.col_idx.data_ptr() if self.num_blocks else 0,
+                    self.values.data_ptr() if self.num_blocks else 0)
+
+
+def spmm_csr(kernel: str, A: DeviceCSR, B, C=None, stream=None):
+    """Launch one of the seven CSR entry points (reference src/kernels/spmm_*.h).
+
+    B: cuda float32 tensor (K x N), C: optional cuda float32 (M x N) output."""
+    torch = _torch()
+    if kernel not in CSR_KERNELS:
+        raise SpmmError(SPMM_INVALID, f"unknown CSR kernel {kernel!r}")
+    N = int(B.shape[1]) if B.dim() == 2 else 0
+    if C is None:
+        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B.device)
+    s = A.struct()
+    fn = getattr(lib(), f"spmm_c_{kernel}")
+    _check(fn(ctypes.byref(s), B.data_ptr(), C.data_ptr(), N, _stream_handle(stream)))
+    return C
+
+
+def spmm_tiled_v3_partitioned(A: DeviceCSR, bounds, B, C=None, stream=None):
+    torch = _torch()
+    N = int(B.shape[1])
+    if C is None:
+        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B.device)
+    s = A.struct()
+    _check(lib().spmm_c_tiled_v3_partitioned(ctypes.byref(s), bounds.data_ptr(),
+                                             int(bounds.numel()) - 1, B.data_ptr(),
+                                             C.data_ptr(), N, _stream_handle(stream)))
+    return C
+
+
+def spmm_tiled_v3_opts(A: DeviceCSR, B, opts: EngineOptsT, C=None, stream=None):
+    torch = _torch()
+    N = int(B.shape[1])
+    if C is None:
+        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B.device)
+    s = A.struct()
+    _check(lib().spmm_c_tiled_v3_opts(ctypes.byref(s), B.data_ptr(), C.data_ptr(), N,
+                                      ctypes.byref(opts), _stream_handle(stream)))
+    return C
+
+
+def float_to_half(src, dst=None, stream=None):
+    """Reference spmm_wmma.cu:125-130: fp32 -> fp16 (RNE) on the device."""
+    torch = _torch()
+    if dst is None:
+        dst = torch.empty(src.shape, dtype=torch.float16, device=src.device)
+    _check(lib().spmm_c_float_to_half(src.data_ptr(), dst.data_ptr(), src.numel(),
+                                      _stream_handle(stream)))
+    return dst
+
+
+def spmm_wmma(A: DeviceBSR, B16, C=None, stream=None):
+    """Reference spmm_wmma.cu:132-142: BSR x fp16 B -> fp32 C on matrix cores."""
+    torch = _torch()
+    N = int(B16.shape[1])
+    if C is None:
+        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B16.device)
+    s = A.struct()
+    _check(lib().spmm_c_wmma(ctypes.byref(s), B16.data_ptr(), C.data_ptr(), N,
+                             _stream_handle(stream)))
+    return C
+
+
+def launch_repeat(kernel: str, A, B, C, reps: int, stream=None) -> None:
+    s = A.struct()
+    _check(lib().spmm_c_launch_repeat(KERNEL_IDS[kernel], ctypes.byref(s), B.data_ptr(),
+                                      C.data_ptr(), int(B.shape[1]), reps, _stream_handle(stream)))
+
+
+def launch_repeat_opts(A: DeviceCSR, B, C, opts: EngineOptsT, reps: int, stream=None) -> None:
+    s = A.struct()
+    _check(lib().spmm_c_launch_repeat_opts(ctypes.byref(s), B.data_ptr(), C.data_ptr(),
+                                           int(B.shape[1]), ctypes.byref(opts), reps,
+                                           _stream_handle(stream)))
+
+
+def time_repeat(kernel: str, A, B, C, reps: int, stream=None) -> float:
+    """Milliseconds for `reps` back-to-back launches between two hipEvents on `stream`."""
+    s = A.struct()
+    ms = ctypes.c_float()
+    _check(lib().spmm_c_time_repeat(KERNEL_IDS[kernel], ctypes.byref(s), B.data_ptr(),
+                                    C.data_ptr(), int(B.shape[1]), reps, _stream_handle(stream),
+                                    ctypes.byref(ms)))
+    return ms.value

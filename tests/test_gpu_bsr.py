@@ -1,0 +1,145 @@
+"""GPU parity of the BSR / matrix-core path (roles of spmm_wmma.cu) and of the
+fp32 -> fp16 conversion, against the oracle, through the C ABI on cuda:0.
+
+Bar (north star): within 1e-2 relative of fp32 accumulation of the same
+fp16-rounded inputs (gpu_util.check_bsr).  A second, much tighter check
+against the exact (fp64) product of the fp16 operands catches operand-layout
+mistakes that a loose bar could hide.
+"""
+import numpy as np
+import pytest
+
+from gpu_util import check_bsr, check_csr, make_config
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "GPU tests need cuda:0"
+    return t
+
+
+def _refs(S, O, A, B):
+    """(host BSR, fp16 bits of B, oracle fp32 result, fp64 exact, |A16||B16|)."""
+    hb = S.bsr_from_csr_host(A)
+    B16 = O.f32_to_f16(B)
+    C32 = O.bsr_spmm_f32(A.num_rows, A.num_cols, hb.row_ptr, hb.col_idx, hb.values, B16, threads=16)
+    A16 = A.values.astype(np.float16).astype(np.float32)
+    Bh = B16.view(np.float16).astype(np.float32)
+    C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A16, Bh, threads=16)
+    return hb, B16, C32, C64, absC
+
+
+def _run_wmma(S, torch, hb, B16):
+    dA = S.DeviceBSR(hb)
+    dB = torch.from_numpy(B16.view(np.int16)).cuda()
+    dC = torch.full((hb.num_rows, B16.shape[1]), float("nan"), device="cuda")
+    S.spmm_wmma(dA, dB, dC)
+    torch.cuda.synchronize()
+    return dC.cpu().numpy()
+
+
+def _no_duplicates(A):
+    for r in range(A.num_rows):
+        row = A.col_idx[A.row_ptr[r]:A.row_ptr[r + 1]]
+        if np.unique(row).size != row.size:
+            return False
+    return True
+
+
+def _cases(S):
+    rng = np.random.default_rng(99)
+    out = {}
+    out["single_block"] = (S.csr_from_coo_host(16, 16, np.repeat(np.arange(16), 16),
+                                                np.tile(np.arange(16), 16),
+                                                rng.uniform(-1, 1, 256)),
+                           rng.uniform(-1, 1, (16, 16)))
+    out["odd_pair_count"] = (S.generate_banded_csr(48, 48, 1, 5), rng.uniform(-1, 1, (48, 32)))
+    out["ragged_dims"] = (S.generate_uniform_random_csr(45, 70, 0.08, 6),
+                          rng.uniform(-1, 1, (70, 48)))
+    out["n_not_16"] = (S.generate_uniform_random_csr(64, 64, 0.1, 7), rng.uniform(-1, 1, (64, 20)))
+    out["n_1"] = (S.generate_uniform_random_csr(64, 40, 0.1, 8), rng.uniform(-1, 1, (40, 1)))
+    out["empty_block_rows"] = (S.csr_from_coo_host(80, 64, [0, 1, 70], [3, 60, 33], [1, 2, 3]),
+                               rng.uniform(-1, 1, (64, 64)))
+    out["empty"] = (S.csr_from_coo_host(33, 20, [], [], []), rng.uniform(-1, 1, (20, 16)))
+    out["wide_n"] = (S.generate_banded_csr(256, 256, 20, 9), rng.uniform(-1, 1, (256, 320)))
+    out["block_diag_small"] = (S.generate_block_diagonal_csr(512, 512, 64, 10),
+                               rng.uniform(-1, 1, (512, 256)))
+    for k, (A, B) in out.items():
+        A.values = S.round_to_fp16(A.values)
+        out[k] = (A, S.round_to_fp16(np.asarray(B, np.float32)))
+    return out
+
+
+@pytest.mark.parametrize("name", ["single_block", "odd_pair_count", "ragged_dims", "n_not_16",
+                                  "n_1", "empty_block_rows", "empty", "wide_n",
+                                  "block_diag_small"])
+def test_wmma_cases(S, O, torch, name):
+    A, B = _cases(S)[name]
+    assert _no_duplicates(A)
+    hb, B16, C32, C64, absC = _refs(S, O, A, B)
+    say(f"wmma case={name} M={A.num_rows} K={A.num_cols} N={B.shape[1]} blocks={hb.num_blocks}")
+    C = _run_wmma(S, torch, hb, B16)
+    check_bsr(C, C32, absC)
+    # fp16 products are exact in fp32: only fp32 summation error remains
+    check_csr(C, C64, absC, tol=1e-5)
+
+
+@pytest.mark.parametrize("cfg", ["c3", "c4"])
+def test_wmma_configs(S, O, torch, cfg):
+    A, B = make_config(S, cfg)
+    hb, B16, C32, C64, absC = _refs(S, O, A, B)
+    say(f"wmma config={cfg} blocks={hb.num_blocks} N={B.shape[1]}")
+    C = _run_wmma(S, torch, hb, B16)
+    rel = check_bsr(C, C32, absC)
+    check_csr(C, C64, absC, tol=1e-5)
+    say(f"  rel_l2 vs fp32 oracle={rel:.3e}")
+
+
+def test_wmma_on_uniform_c1(S, O, torch):
+    # high fill-in input (about 92 stored elements per nonzero) is still exact
+    A, B = make_config(S, "c1")
+    A.values = S.round_to_fp16(A.values)
+    B = S.round_to_fp16(B)
+    hb, B16, C32, C64, absC = _refs(S, O, A, B)
+    say(f"wmma config=c1 blocks={hb.num_blocks}")
+    check_bsr(_run_wmma(S, torch, hb, B16), C32, absC)
+
+
+def test_float_to_half_bitwise(S, O, torch):
+    rng = np.random.default_rng(17)
+    x = np.concatenate([rng.standard_normal(100003).astype(np.float32) * s
+                        for s in (1e-6, 1e-3, 1.0, 1e3, 7e4)])
+    x[:8] = [0.0, -0.0, 65504.0, 65520.0, 1e-8, 5.9604645e-08, 2.9802322e-08, -1.0009766]
+    want = O.f32_to_f16(x)
+    src = torch.from_numpy(x).cuda()
+    say(f"float_to_half n={x.size} aligned")
+    got = S.float_to_half(src).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+    say("float_to_half unaligned view")
+    sub = src[1:]  # 4-byte aligned only: scalar path
+    got2 = S.float_to_half(sub).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got2, want[1:])
+
+
+def test_wmma_argument_errors(S, torch):
+    import ctypes
+    s = S.BsrT(16, 16, 2, 1, 0, 0, 0, 0, 0)  # block_rows inconsistent with num_rows
+    assert S.lib().spmm_c_wmma(ctypes.byref(s), 0, 0, 16, None) == S.SPMM_INVALID
+
+
+def test_wmma_linearity_c4(S, O, torch):
+    A, B = make_config(S, "c4")
+    hb = S.bsr_from_csr_host(A)
+    dA = S.DeviceBSR(hb)
+    B16 = torch.from_numpy(O.f32_to_f16(B).view(np.int16)).cuda().view(torch.float16)
+    say("wmma linearity c4")
+    c1 = S.spmm_wmma(dA, B16)
+    c2 = S.spmm_wmma(dA, B16 * 2)
+    assert torch.equal(c2, c1 * 2)

@@ -1,0 +1,47 @@
+"""Hybrid dispatch end to end on the GPU (spmm_hybrid.cu:32-125): the plan on
+each BASELINE config, host-in/host-out execution of the chosen back end, and
+the parity of its result."""
+import numpy as np
+import pytest
+
+from gpu_util import CONFIGS, check_bsr, check_csr, make_config
+
+pytestmark = pytest.mark.gpu
+
+EXPECTED_BACKEND = {"c1": "csr", "c2": "csr", "c3": "wmma", "c4": "wmma", "c5": "csr"}
+
+
+@pytest.mark.parametrize("cfg", sorted(CONFIGS))
+def test_hybrid_plan_and_run(S, O, cfg):
+    A, B = make_config(S, cfg)
+    N = B.shape[1]
+    plan = S.hybrid_choose(A, N)
+    print(f"hybrid config={cfg} backend={plan.backend_name} fill={plan.fill_in_ratio:.4f}",
+          flush=True)
+    assert plan.backend_name == EXPECTED_BACKEND[cfg]
+    C, ms = S.hybrid_run(plan, A, B, warmup=1, iters=3)
+    assert ms > 0
+    if plan.backend_name == "csr":
+        C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=16)
+        check_csr(C, C64, absC)
+    else:
+        hb = S.bsr_from_csr_host(A)
+        B16 = O.f32_to_f16(B)
+        C32 = O.bsr_spmm_f32(A.num_rows, A.num_cols, hb.row_ptr, hb.col_idx, hb.values, B16,
+                             threads=16)
+        _, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values,
+                                 B16.view(np.float16).astype(np.float32), threads=16)
+        check_bsr(C, C32, absC)
+
+
+def test_hybrid_forced_backends_agree(S, O):
+    # both back ends on the same fp16-exact input give the same product
+    A, B = make_config(S, "c3")
+    csr = S.hybrid_choose(A, B.shape[1], threshold=0.5)   # fill 1.1158 > 0.5 -> CSR
+    mma = S.hybrid_choose(A, B.shape[1], threshold=2.0)
+    assert csr.backend_name == "csr" and mma.backend_name == "wmma"
+    C1, _ = S.hybrid_run(csr, A, B, warmup=0, iters=1)
+    C2, _ = S.hybrid_run(mma, A, B, warmup=0, iters=1)
+    C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=16)
+    check_csr(C1, C64, absC)
+    check_csr(C2, C64, absC)

@@ -129,6 +129,22 @@ def library_path() -> str:
     return LIB_PATH
 
 
+def _adopt_torch_hip_runtime() -> None:
+    """Make the process hold exactly one HIP runtime.
+
+    torch bundles its own libamdhip64 (SONAME libamdhip64.so.7) and loads it by
+    a different file name than the system one.  If libspmm_amd.so is loaded
+    first, the system runtime comes in with it and torch later brings a second
+    copy; the two cannot share the device (launches then fail with "no
+    ROCm-capable device").  Importing torch first makes the dynamic loader
+    resolve the engine's libamdhip64.so.7 dependency to torch's copy.
+    """
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def lib() -> ctypes.CDLL:
     """Load libspmm_amd.so (built by ``make -C sparse-matrix-multiplication_amd``)."""
     global _lib
@@ -136,6 +152,7 @@ def lib() -> ctypes.CDLL:
         if not os.path.exists(LIB_PATH):
             raise SpmmError(SPMM_INVALID, f"{LIB_PATH} is not built; run "
                             "`make -C sparse-matrix-multiplication_amd` (or __graft_entry__.build())")
+        _adopt_torch_hip_runtime()
         handle = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in _SIGNATURES.items():
             fn = getattr(handle, name)

@@ -1,0 +1,67 @@
+"""The C-ABI library loads without a GPU and exports every symbol that
+include/spmm_capi.h declares, plus the C++ drop-in API of the reference
+(namespace spmm); the drivers are built."""
+import os
+import re
+import subprocess
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "spmm_capi.h")
+BUILD = os.path.join(ROOT, "sparse-matrix-multiplication_amd", "build")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(spmm_c_\w+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(S):
+    names = declared_functions()
+    assert len(names) >= 40
+    lib = S.lib()
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_covers_the_header(S):
+    assert set(declared_functions()) == set(S._SIGNATURES)
+
+
+def test_cpp_api_is_exported(S):
+    out = subprocess.run(["nm", "-DC", "--defined-only", S.library_path()], check=True,
+                         capture_output=True, text=True).stdout
+    for sym in ("spmm::csr_alloc_host(int, int, int)",
+                "spmm::csr_free_host(spmm::CSR&)",
+                "spmm::generate_uniform_random_csr(int, int, float, int)",
+                "spmm::csr_to_device(spmm::CSR const&)",
+                "spmm::bsr_from_csr_host(spmm::CSR const&)",
+                "spmm::bsr_compute_stats(spmm::BSR_host const&)",
+                "spmm::spmm_baseline(spmm::CSR const&, float const*, float*, int)",
+                "spmm::spmm_memopt(spmm::CSR const&, float const*, float*, int)",
+                "spmm::spmm_memopt_v2(spmm::CSR const&, float const*, float*, int)",
+                "spmm::spmm_tiled(spmm::CSR const&, float const*, float*, int)",
+                "spmm::spmm_tiled_v2(spmm::CSR const&, float const*, float*, int)",
+                "spmm::spmm_tiled_v3(spmm::CSR const&, float const*, float*, int)",
+                "spmm::spmm_tiled_v4(spmm::CSR const&, float const*, float*, int)",
+                "spmm::spmm_wmma(spmm::BSR const&, __half const*, float*, int)",
+                "spmm::float_to_half(float const*, __half*, int)",
+                "spmm::hybrid_choose(spmm::CSR const&, int, float)",
+                "spmm::backend_name(spmm::Backend)",
+                "spmm::spmm_hybrid_run(spmm::HybridPlan const&, spmm::CSR const&, float const*, "
+                "float*, int, int, int)"):
+        assert sym in out, sym
+
+
+def test_drivers_built_and_print_usage():
+    for exe in ("spmm_bench", "spmm_run"):
+        path = os.path.join(BUILD, exe)
+        assert os.access(path, os.X_OK), path
+        r = subprocess.run([path, "--help"], capture_output=True, text=True, timeout=60)
+        assert r.returncode == 0 and "--kernel" in r.stderr if exe == "spmm_bench" else True
+        bad = subprocess.run([path, "--bogus"], capture_output=True, text=True, timeout=60)
+        assert bad.returncode != 0 and "unknown option" in bad.stderr
+
+
+def test_version_string(S):
+    assert b"gfx950" in S.lib().spmm_c_version()

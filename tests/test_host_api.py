@@ -1,0 +1,214 @@
+"""The engine's host side (C++ API through the C ABI, no GPU needed) against
+the oracle and the reference's documented behaviour: generators, COO->CSR,
+binary format, row slices, BSR build and statistics, dispatch, partition and
+metrics, and the error conditions the reference raises."""
+import os
+import struct
+
+import numpy as np
+import pytest
+
+
+def test_uniform_generator_bitwise_equals_oracle(S, O):
+    for (m, k, d, seed) in ((1024, 1024, 0.01, 42), (300, 700, 0.05, 9), (64, 1, 0.5, 3)):
+        A = S.generate_uniform_random_csr(m, k, d, seed)
+        rp, ci, va = O.uniform_csr(m, k, d, seed)
+        assert np.array_equal(A.row_ptr, rp)
+        assert np.array_equal(A.col_idx, ci)
+        assert np.array_equal(A.values.view(np.uint32), va.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,d,nnz", [(4096, 0.01, 167686), (8192, 0.01, 671114),
+                                     (4096, 0.05, 839236)])
+def test_uniform_generator_known_nnz(S, m, d, nnz):
+    assert S.generate_uniform_random_csr(m, m, d, 42).nnz == nnz
+
+
+def test_uniform_generator_rejects_bad_density(S):
+    for d in (-0.1, 1.5, float("nan")):
+        with pytest.raises(S.SpmmError) as e:
+            S.generate_uniform_random_csr(10, 10, d, 1)
+        assert "invalid density" in str(e.value)
+    assert S.generate_uniform_random_csr(5, 7, 1.0, 1).nnz == 35
+    assert S.generate_uniform_random_csr(5, 7, 0.0, 1).nnz == 0
+
+
+def test_dense_generator_bitwise_equals_oracle(S, O):
+    a = S.generate_dense_row_major(129, 77, 43)
+    assert np.array_equal(a.view(np.uint32), O.dense(129, 77, 43).view(np.uint32))
+
+
+def test_coo_to_csr_matches_oracle(S, O):
+    rng = np.random.default_rng(8)
+    n = 4000
+    r = rng.integers(0, 150, n)
+    c = rng.integers(0, 90, n)
+    r[:100], c[:100] = r[100:200], c[100:200]
+    v = rng.standard_normal(n).astype(np.float32)
+    A = S.csr_from_coo_host(150, 90, r, c, v)
+    rp, ci, va = O.coo_to_csr(150, r, c, v)
+    assert np.array_equal(A.row_ptr, rp) and np.array_equal(A.col_idx, ci)
+    assert np.array_equal(A.values, va) and A.nnz == n
+
+
+def test_coo_errors(S):
+    with pytest.raises(S.SpmmError):
+        S.csr_from_coo_host(3, 3, [0, 1], [0], [1.0, 2.0])
+    with pytest.raises(S.SpmmError):
+        S.csr_from_coo_host(3, 3, [0, 3], [0, 0], [1.0, 2.0])  # row out of range
+
+
+def test_binary_format_round_trip_and_layout(S, tmp_path):
+    A = S.generate_uniform_random_csr(50, 60, 0.1, 5)
+    path = str(tmp_path / "a.bin")
+    S.csr_write_binary_host(A, path)
+    raw = open(path, "rb").read()
+    hdr = struct.unpack("<iii", raw[:12])
+    assert hdr == (50, 60, A.nnz)
+    assert len(raw) == 12 + 4 * 51 + 8 * A.nnz
+    body = np.frombuffer(raw[12:], dtype=np.uint8)
+    assert np.array_equal(body[:4 * 51].view("<i4"), A.row_ptr)
+    assert np.array_equal(body[4 * 51:4 * 51 + 4 * A.nnz].view("<i4"), A.col_idx)
+    assert np.array_equal(body[4 * 51 + 4 * A.nnz:].view("<f4"), A.values)
+    B = S.csr_read_binary_host(path)
+    assert np.array_equal(B.row_ptr, A.row_ptr) and np.array_equal(B.col_idx, A.col_idx)
+    assert np.array_equal(B.values, A.values) and (B.num_rows, B.num_cols) == (50, 60)
+
+
+def test_binary_format_errors(S, tmp_path):
+    with pytest.raises(S.SpmmError) as e:
+        S.csr_read_binary_host(str(tmp_path / "missing.bin"))
+    assert e.value.code == S.SPMM_IO_ERROR and "cannot open" in str(e.value)
+    short = tmp_path / "short.bin"
+    short.write_bytes(struct.pack("<ii", 1, 2))
+    with pytest.raises(S.SpmmError) as e:
+        S.csr_read_binary_host(str(short))
+    assert "short read on header" in str(e.value)
+    body = tmp_path / "body.bin"
+    body.write_bytes(struct.pack("<iii", 4, 4, 10) + b"\0" * 8)
+    with pytest.raises(S.SpmmError) as e:
+        S.csr_read_binary_host(str(body))
+    assert "short read on body" in str(e.value)
+
+
+def test_row_slice(S):
+    A = S.generate_uniform_random_csr(40, 30, 0.2, 2)
+    s = S.csr_row_slice_host(A, 10, 25)
+    assert s.num_rows == 15 and s.num_cols == 30
+    assert s.row_ptr[0] == 0 and s.nnz == A.row_ptr[25] - A.row_ptr[10]
+    assert np.array_equal(s.to_dense(), A.to_dense()[10:25])
+    assert S.csr_row_slice_host(A, 5, 5).nnz == 0
+    for bad in ((-1, 3), (3, 41), (20, 10)):
+        with pytest.raises(S.SpmmError) as e:
+            S.csr_row_slice_host(A, *bad)
+        assert "invalid row range" in str(e.value)
+
+
+def test_bsr_build_equals_oracle(S, O):
+    rng = np.random.default_rng(12)
+    for (M, K) in ((1024, 1024), (45, 70), (17, 300)):
+        A = S.generate_uniform_random_csr(M, K, 0.03, int(rng.integers(1000)))
+        b = S.bsr_from_csr_host(A)
+        brp, bci, bv = O.bsr_build(M, K, A.row_ptr, A.col_idx, A.values)
+        assert np.array_equal(b.row_ptr, brp) and np.array_equal(b.col_idx, bci)
+        assert np.array_equal(b.values, bv)
+        assert (b.block_rows, b.block_cols) == ((M + 15) // 16, (K + 15) // 16)
+
+
+def test_bsr_duplicates_keep_last(S, O):
+    A = S.csr_from_coo_host(20, 20, [3, 3, 3], [4, 4, 9], [1.0, 2.0, 3.0])
+    b = S.bsr_from_csr_host(A)
+    blk = b.values.view(np.float16).reshape(-1, 16, 16)[0].astype(np.float32)
+    assert blk[3, 4] == 2.0 and blk[3, 9] == 3.0
+
+
+@pytest.mark.parametrize("m,d,known", [(4096, 0.01, (60630, 15521280, 92.6, 0.925)),
+                                       (1024, 0.05, (4096, 1048576, 20.1, 1.0))])
+def test_bsr_stats_known_answers(S, m, d, known):
+    st = S.bsr_compute_stats(S.bsr_from_csr_host(S.generate_uniform_random_csr(m, m, d, 42)))
+    assert (st.num_blocks, st.stored_elements) == known[:2]
+    assert round(st.fill_in_ratio, 1) == known[2] and round(st.block_density, 3) == known[3]
+
+
+def test_config_patterns(S):
+    b = S.generate_banded_csr(8192, 8192, 64, 1003)
+    assert b.nnz == 1052608
+    st = S.bsr_compute_stats(S.bsr_from_csr_host(b))
+    assert st.num_blocks == 4588 and round(st.fill_in_ratio, 4) == 1.1158
+    rows = np.repeat(np.arange(8192), np.diff(b.row_ptr))
+    assert np.all(np.abs(rows - b.col_idx) <= 64)
+    d = S.generate_block_diagonal_csr(8192, 8192, 256, 2003, 0.1)
+    assert d.nnz == 32 * 256 * 256
+    st = S.bsr_compute_stats(S.bsr_from_csr_host(d))
+    assert st.num_blocks == 8192 and st.fill_in_ratio == 1.0
+    assert np.all(d.col_idx // 256 == np.repeat(np.arange(8192), 256) // 256)
+    assert abs(float(d.values.std()) - 0.1) < 0.002 and abs(float(d.values.mean())) < 0.002
+    p = S.generate_power_law_csr(16384, 16384, 164.0, 1.5, 4096, 3003)
+    deg = np.diff(p.row_ptr)
+    assert deg.max() == 4096 and deg.min() >= 1
+    assert 0.008 < p.nnz / 16384**2 < 0.011
+    for r in (0, int(np.argmax(deg)), 16383):
+        row = p.col_idx[p.row_ptr[r]:p.row_ptr[r + 1]]
+        assert np.all(np.diff(row) > 0)  # distinct, sorted
+    # power-law tail: a heavy top percentile
+    top = np.sort(deg)[-164:].sum() / p.nnz
+    assert top > 0.1
+
+
+def test_power_law_small_distribution(S):
+    # Pareto x_m = 1, alpha: P(x > t) = t^-alpha before scaling; degree ratios
+    # to the minimum follow the same tail
+    p = S.generate_power_law_csr(200000, 100000, 20.0, 2.5, 100000, 11)
+    deg = np.diff(p.row_ptr).astype(np.float64)
+    x = deg / deg.min()
+    for t in (2.0, 4.0):
+        frac = float(np.mean(x > t))
+        assert abs(frac - t ** -2.5) < 0.02, (t, frac)
+
+
+def test_round_to_fp16(S):
+    x = np.array([1.0, 1.0004883, 65520.0, 1e-8, -2.5], np.float32)
+    assert np.array_equal(S.round_to_fp16(x), x.astype(np.float16).astype(np.float32))
+
+
+def test_hybrid_choose_matches_oracle_rule(S, O):
+    A = S.generate_banded_csr(256, 256, 3, 1)
+    fill = S.bsr_compute_stats(S.bsr_from_csr_host(A)).fill_in_ratio
+    reasons = {0: "low BSR fill-in and N aligned to 16 -> Tensor Cores",
+               1: "N not a multiple of 16 -> CUDA-core CSR",
+               2: "high BSR fill-in -> CUDA-core CSR"}
+    for N in (0, 8, 16, 17, 128):
+        for thr in (1.0, fill, 2.0, 6.0):
+            p = S.hybrid_choose(A, N, thr)
+            use, why = O.hybrid_rule(fill, N, thr)
+            assert p.backend == use and p.reason == reasons[why], (N, thr)
+            assert p.n_aligned == (N > 0 and N % 16 == 0)
+            assert p.fill_in_ratio == pytest.approx(fill)
+    assert S.backend_name(0) == "csr" and S.backend_name(1) == "wmma"
+    assert S.hybrid_default_threshold() > 1.0
+
+
+def test_nnz_balanced_bounds_equals_oracle(S, O):
+    A = S.generate_power_law_csr(3000, 3000, 30.0, 1.5, 1000, 4)
+    for parts in (1, 2, 7, 256, 4000):
+        assert np.array_equal(S.nnz_balanced_bounds(A, parts), O.nnz_balanced_bounds(A.row_ptr, parts))
+    with pytest.raises(S.SpmmError):
+        S.nnz_balanced_bounds(A, 0)
+    assert 256 <= S.default_partition_parts(16384, 2_500_000) <= 16384
+    assert S.default_partition_parts(10, 100) == 10
+
+
+def test_compare_equals_oracle(S, O):
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal(5000).astype(np.float32)
+    b = a + rng.standard_normal(5000).astype(np.float32) * 1e-3
+    assert np.allclose(S.compare(a, b), O.compare(a, b), rtol=1e-6)
+
+
+def test_host_reference_equals_oracle(S, O):
+    A = S.generate_power_law_csr(500, 800, 30.0, 1.5, 400, 6)
+    B = S.generate_dense_row_major(800, 48, 7)
+    C64, _ = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=2)
+    for threads in (1, 3):
+        C = S.host_reference_f64(A, B, threads)
+        assert np.array_equal(C, C64.astype(np.float32))

@@ -84,9 +84,10 @@ typedef struct spmm_hybrid_plan_t {
  * row-block engine's compile-time variants for measurement sweeps. */
 typedef struct spmm_engine_opts_t {
     int vec;            /* floats per lane per B load: 1, 2, 4 */
-    int waves;          /* waves per workgroup: 4, 8 */
-    int unroll;         /* B rows in flight per wave: 8, 16 */
+    int waves;          /* waves per workgroup: 2, 4, 8 */
+    int unroll;         /* B row segments in flight per lane per step: 8, 16 */
     int rows_per_block; /* implicit partition granularity */
+    int groups;         /* lane groups per wave, entries interleaved: 1, 2, 4 */
 } spmm_engine_opts_t;
 
 const char* spmm_c_last_error(void);

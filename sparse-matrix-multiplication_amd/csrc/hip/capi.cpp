@@ -147,6 +147,7 @@ spmm::engine::EngineOpts opts_from_c(const spmm_engine_opts_t* o) {
         e.waves          = o->waves;
         e.unroll         = o->unroll;
         e.rows_per_block = o->rows_per_block;
+        e.groups         = o->groups;
     }
     return e;
 }

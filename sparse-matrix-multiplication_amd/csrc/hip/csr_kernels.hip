@@ -100,22 +100,31 @@ __global__ __launch_bounds__(256, MIN_WAVES_PER_EU) void csr_wave_per_row(
 // those rows are cut into WAVES equal contiguous ranges, one per wave, so a
 // long row is shared by several waves and many short rows by one wave.
 //
-// Per wave.  The wave streams its range in 64-entry chunks: lane q holds
-// (col_idx, value) of entry q in VGPRs and v_readlane broadcasts entry after
-// entry into SGPRs.  For each entry the wave loads the B row segment
-// B[k, c0 .. c0 + 64*VEC) (VEC floats per lane, UNROLL rows in flight) and
-// accumulates into a per-lane register tile.  A row boundary flushes the tile:
+// Lane groups.  A wave is split into G groups of 64/G lanes; each group covers
+// one column tile of COLS = (64/G) * VEC columns with VEC-float (up to 16-byte)
+// loads, and the groups take interleaved entries of the wave's range (group h
+// takes entries h, h+G, h+2G, ...).  One load instruction therefore fetches G
+// different B row segments: for N = 128 fp32, G = 2 and each half-wave reads
+// one 512-byte row with dwordx4 loads, which is what the gfx950 vector memory
+// pipe serves fastest for random row gathers.
+//
+// Per wave.  The range is streamed in 64-entry chunks held in VGPRs (lane q
+// holds col_idx / value of entry q; the next chunk is prefetched while the
+// current one is consumed).  v_readlane broadcasts the entries of a step to
+// their groups, U row segments per lane are in flight per step, and every
+// lane accumulates into a VEC-wide register tile.  At a row boundary the
+// groups' tiles are summed with cross-lane shuffles and the row is flushed:
 //   - a row that lies wholly inside the wave's range is stored to C;
 //   - the first row of a range that started in an earlier wave goes to an LDS
 //     slot (s_part[wave]);
 //   - the last row of a range that continues in a later wave stays in the
 //     registers of its owner, which after a barrier adds the LDS slots of the
 //     following waves in wave order and stores it.
-// The sum order is therefore fixed by the partition: results are
-// deterministic run to run.
+// The sum order is fixed by the partition and the launch shape, so results
+// are deterministic run to run.
 //
 // Rows of the workgroup without nonzeros are zero-filled up front.  Row
-// pointers are staged in LDS in windows of RP_CAP rows.
+// pointers are staged in LDS in windows of kRpCap rows.
 // ---------------------------------------------------------------------------
 struct RowblockArgs {
     const int*   row_ptr;
@@ -132,26 +141,63 @@ struct RowblockArgs {
 constexpr int kRpCap = 1024;
 
 template <int VEC>
-__device__ __forceinline__ void store_cols(float* crow, int col, bool col_ok,
-                                           typename Vec<VEC>::T v) {
-    if (col_ok) {
-        __builtin_nontemporal_store(v, reinterpret_cast<typename Vec<VEC>::T*>(crow + col));
+__device__ __forceinline__ void store_vec(float* p, typename Vec<VEC>::T v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<typename Vec<VEC>::T*>(p));
+}
+
+// Value of x held by lane q + (this lane's group), for groups of 64/G lanes.
+template <int G>
+__device__ __forceinline__ int pick(int x, int q, int grp) {
+    int r = __builtin_amdgcn_readlane(x, q);
+#pragma unroll
+    for (int h = 1; h < G; ++h) {
+        const int t = __builtin_amdgcn_readlane(x, q + h);
+        r = grp == h ? t : r;
+    }
+    return r;
+}
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m); }
+
+// Sum of the G groups' tiles, returned to every lane.
+template <int VEC, int G>
+__device__ __forceinline__ typename Vec<VEC>::T reduce_groups(typename Vec<VEC>::T v) {
+    if constexpr (G == 1) {
+        return v;
+    } else {
+        using VT = typename Vec<VEC>::T;
+#pragma unroll
+        for (int m = kWave / G; m < kWave; m <<= 1) {
+            VT o;
+            if constexpr (VEC == 1) {
+                o = shfl_xor_f(v, m);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) o[e] = shfl_xor_f(v[e], m);
+            }
+            v += o;
+        }
+        return v;
     }
 }
 
-template <int VEC, int WAVES, int UNROLL>
+template <int VEC, int G, int WAVES, int U>
 __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
     using VT = typename Vec<VEC>::T;
-    constexpr int COLS = kWave * VEC;
-    static_assert(kWave % UNROLL == 0, "UNROLL must divide the wave size");
+    constexpr int LPG  = kWave / G;   // lanes per group
+    constexpr int COLS = LPG * VEC;   // columns per pass
+    constexpr int STEP = U * G;       // entries per step
+    static_assert(kWave % STEP == 0, "U * G must divide the wave size");
 
-    __shared__ int   s_rp[kRpCap + 1];
-    __shared__ VT    s_part[WAVES][kWave];
-    __shared__ int   s_first[WAVES];
+    __shared__ int s_rp[kRpCap + 1];
+    __shared__ VT  s_part[WAVES][LPG];
+    __shared__ int s_first[WAVES];
 
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int N = a.N;
+    const int lane  = threadIdx.x & (kWave - 1);
+    const int wave  = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp   = lane / LPG;
+    const int glane = lane % LPG;
+    const int N     = a.N;
 
     int r_begin, r_end;
     if (a.bounds != nullptr) {
@@ -176,7 +222,7 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
                 const int b = __builtin_ctzll(empty);
                 empty &= empty - 1;
                 float* crow = a.C + static_cast<size_t>(w0 + base + b) * N;
-                for (int c = lane * VEC; c < N; c += COLS) store_cols<VEC>(crow, c, true, vzero<VEC>());
+                for (int c = lane * VEC; c < N; c += kWave * VEC) store_vec<VEC>(crow + c, vzero<VEC>());
             }
         }
 
@@ -198,69 +244,91 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
         }
 
         for (int c0 = 0; c0 < N; c0 += COLS) {
-            const int col = c0 + lane * VEC;
+            const int  col    = c0 + glane * VEC;
             const bool col_ok = col < N;
+            const int  col_ld = col_ok ? col : 0;  // loads stay in bounds; never stored
+            const bool writer = grp == 0 && col_ok;
             if (lane == 0) s_first[wave] = (pa < pb) ? -1 : -2;
 
-            int owner_row = -1;  // local row this wave must finish after the barrier
+            int owner_row = -1;  // local row this wave finishes after the barrier
             VT acc = vzero<VEC>();
             if (pa < pb) {
-                int row = first;
-                int row_stop = s_rp[row + 1];
-                bool head = s_rp[row] < pa;  // row began in an earlier wave
+                int  row      = first;
+                int  row_stop = s_rp[row + 1];
+                bool head     = s_rp[row] < pa;  // row began in an earlier wave
 
+                auto flush = [&]() {
+                    const VT t = reduce_groups<VEC, G>(acc);
+                    if (head) {
+                        if (grp == 0) s_part[wave][glane] = t;
+                        if (lane == 0) s_first[wave] = row;
+                        head = false;
+                    } else if (writer) {
+                        store_vec<VEC>(a.C + static_cast<size_t>(w0 + row) * N + col, t);
+                    }
+                    acc = vzero<VEC>();
+                };
+
+                int   kn = 0;
+                float vn = 0.f;
+                if (lane < min(kWave, pb - pa)) {
+                    kn = __builtin_nontemporal_load(a.col_idx + pa + lane);
+                    vn = __builtin_nontemporal_load(a.vals + pa + lane);
+                }
                 for (int base = pa; base < pb; base += kWave) {
                     const int cnt = min(kWave, pb - base);
-                    int   kc = 0;
-                    float vc = 0.f;
-                    if (lane < cnt) {
-                        kc = __builtin_nontemporal_load(a.col_idx + base + lane);
-                        vc = __builtin_nontemporal_load(a.vals + base + lane);
+                    const int   kc = kn;  // lanes >= cnt hold k = 0 (a valid B row), v = 0
+                    const float vc = vn;
+                    const int nb = base + kWave;
+                    if (nb < pb) {  // prefetch the next chunk
+                        kn = 0;
+                        vn = 0.f;
+                        if (lane < min(kWave, pb - nb)) {
+                            kn = __builtin_nontemporal_load(a.col_idx + nb + lane);
+                            vn = __builtin_nontemporal_load(a.vals + nb + lane);
+                        }
                     }
-                    for (int j = 0; j < cnt; j += UNROLL) {
-                        VT bv[UNROLL];
+                    for (int j = 0; j < cnt; j += STEP) {
+                        VT    bv[U];
+                        float vv[U];
 #pragma unroll
-                        for (int u = 0; u < UNROLL; ++u) {
-                            const int q = j + u;
-                            const int k = __builtin_amdgcn_readlane(kc, q);
-                            const float* brow = a.B + static_cast<size_t>(k) * N;
-                            bv[u] = (q < cnt && col_ok)
-                                        ? *reinterpret_cast<const VT*>(brow + col)
-                                        : vzero<VEC>();
+                        for (int u = 0; u < U; ++u) {
+                            const int q = j + u * G;
+                            const int k = pick<G>(kc, q, grp);
+                            vv[u] = __builtin_bit_cast(float, pick<G>(__builtin_bit_cast(int, vc), q, grp));
+                            bv[u] = *reinterpret_cast<const VT*>(a.B + static_cast<size_t>(k) * N + col_ld);
                         }
 #pragma unroll
-                        for (int u = 0; u < UNROLL; ++u) {
-                            const int q = j + u;
-                            if (q < cnt) {
-                                const int pos = base + q;
-                                if (pos >= row_stop) {
-                                    if (head) {
-                                        s_part[wave][lane] = acc;
-                                        if (lane == 0) s_first[wave] = row;
-                                        head = false;
-                                    } else {
-                                        store_cols<VEC>(a.C + static_cast<size_t>(w0 + row) * N,
-                                                        col, col_ok, acc);
+                        for (int u = 0; u < U; ++u) {
+                            const int q0 = j + u * G;
+                            const int p0 = base + q0;
+                            if (q0 + G <= cnt && p0 + G <= row_stop) {
+                                acc = vv[u] * bv[u] + acc;  // all G entries valid, same row
+                            } else {
+#pragma unroll
+                                for (int h = 0; h < G; ++h) {
+                                    if (q0 + h >= cnt) break;  // past the end of the range
+                                    const int P = p0 + h;
+                                    if (P >= row_stop) {
+                                        flush();
+                                        // bounded by the window even for a malformed row_ptr
+                                        do {
+                                            ++row;
+                                            row_stop = s_rp[row + 1];
+                                        } while (row_stop <= P && row < nr - 1);
                                     }
-                                    acc = vzero<VEC>();
-                                    // bounded by the window even for a malformed row_ptr
-                                    do {
-                                        ++row;
-                                        row_stop = s_rp[row + 1];
-                                    } while (row_stop <= pos && row < nr - 1);
+                                    if (grp == h) acc = vv[u] * bv[u] + acc;
                                 }
-                                const float v = __builtin_bit_cast(
-                                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, vc), q));
-                                acc = v * bv[u] + acc;
                             }
                         }
                     }
                 }
                 // The row being accumulated when the range ends.
+                acc = reduce_groups<VEC, G>(acc);
                 if (row_stop == pb && !head) {
-                    store_cols<VEC>(a.C + static_cast<size_t>(w0 + row) * N, col, col_ok, acc);
+                    if (writer) store_vec<VEC>(a.C + static_cast<size_t>(w0 + row) * N + col, acc);
                 } else if (head) {
-                    s_part[wave][lane] = acc;
+                    if (grp == 0) s_part[wave][glane] = acc;
                     if (lane == 0) s_first[wave] = row;
                 } else {
                     owner_row = row;
@@ -272,9 +340,9 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
                     const int f = s_first[w];
                     if (f == -2) continue;
                     if (f != owner_row) break;
-                    acc += s_part[w][lane];
+                    acc += s_part[w][glane];
                 }
-                store_cols<VEC>(a.C + static_cast<size_t>(w0 + owner_row) * N, col, col_ok, acc);
+                if (writer) store_vec<VEC>(a.C + static_cast<size_t>(w0 + owner_row) * N + col, acc);
             }
             __syncthreads();  // s_part / s_first are rewritten by the next column pass
         }
@@ -298,47 +366,63 @@ bool aligned(const void* p, size_t bytes) {
     return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
 
-// Largest VEC the shapes allow: every lane's VEC floats must be in one row and
-// naturally aligned.
+// Widest VEC (<= want, 4 when want == 0) that keeps every lane's VEC floats
+// inside one row and naturally aligned.
 int pick_vec(int N, const float* B, float* C, int want) {
-    auto fits = [&](int v) {
-        return N % v == 0 && aligned(B, sizeof(float) * v) && aligned(C, sizeof(float) * v);
-    };
-    if (want == 0) {
-        // one column pass when possible, widest loads otherwise
-        want = N <= 64 ? 1 : (N <= 128 ? 2 : 4);
-    }
+    if (want == 0) want = 4;
     for (int v = want; v > 1; v >>= 1) {
-        if (fits(v)) return v;
+        if (N % v == 0 && aligned(B, sizeof(float) * v) && aligned(C, sizeof(float) * v)) return v;
     }
     return 1;
 }
 
-template <int VEC, int WAVES, int UNROLL>
+// Groups per wave: enough lanes per group to cover N in one pass, at most 4
+// groups (16 lanes) and at least 1 (64 lanes, several passes for wide N).
+int pick_groups(int N, int vec, int want) {
+    if (want == 1 || want == 2 || want == 4) return want;
+    const int lanes = (N + vec - 1) / vec;
+    if (lanes <= 16) return 4;
+    if (lanes <= 32) return 2;
+    return 1;
+}
+
+template <int VEC, int G, int WAVES, int U>
 hipError_t run_rowblock(const RowblockArgs& args, int grid, hipStream_t stream) {
-    hipLaunchKernelGGL((csr_rowblock<VEC, WAVES, UNROLL>), dim3(grid), dim3(WAVES * kWave), 0,
+    hipLaunchKernelGGL((csr_rowblock<VEC, G, WAVES, U>), dim3(grid), dim3(WAVES * kWave), 0,
                        stream, args);
     return hipGetLastError();
 }
 
-template <int VEC>
-hipError_t dispatch_waves_unroll(int waves, int unroll, const RowblockArgs& args, int grid,
-                                 hipStream_t stream) {
+template <int VEC, int G>
+hipError_t dispatch_shape(int waves, int unroll, const RowblockArgs& args, int grid,
+                          hipStream_t stream) {
     if (waves == 8) {
-        return unroll == 8 ? run_rowblock<VEC, 8, 8>(args, grid, stream)
-                           : run_rowblock<VEC, 8, 16>(args, grid, stream);
+        return unroll == 16 ? run_rowblock<VEC, G, 8, 16>(args, grid, stream)
+                            : run_rowblock<VEC, G, 8, 8>(args, grid, stream);
     }
-    return unroll == 8 ? run_rowblock<VEC, 4, 8>(args, grid, stream)
-                       : run_rowblock<VEC, 4, 16>(args, grid, stream);
+    if (waves == 2) {
+        return unroll == 16 ? run_rowblock<VEC, G, 2, 16>(args, grid, stream)
+                            : run_rowblock<VEC, G, 2, 8>(args, grid, stream);
+    }
+    return unroll == 16 ? run_rowblock<VEC, G, 4, 16>(args, grid, stream)
+                        : run_rowblock<VEC, G, 4, 8>(args, grid, stream);
+}
+
+template <int VEC>
+hipError_t dispatch_groups(int groups, int waves, int unroll, const RowblockArgs& args, int grid,
+                           hipStream_t stream) {
+    if (groups == 4) return dispatch_shape<VEC, 4>(waves, unroll, args, grid, stream);
+    if (groups == 2) return dispatch_shape<VEC, 2>(waves, unroll, args, grid, stream);
+    return dispatch_shape<VEC, 1>(waves, unroll, args, grid, stream);
 }
 
 }  // namespace
 
 int default_partition_parts(int num_rows, int nnz) {
-    // About 1024 nonzeros per workgroup, at least one workgroup per CU and at
-    // most one per row.
-    long parts = (static_cast<long>(nnz) + 1023) / 1024;
-    parts = std::max<long>(parts, 256);
+    // About 640 nonzeros per workgroup (80 per wave of the default 8-wave
+    // shape), at least two workgroups per CU and at most one per row.
+    long parts = (static_cast<long>(nnz) + 639) / 640;
+    parts = std::max<long>(parts, 512);
     parts = std::min<long>(parts, std::max(num_rows, 1));
     return static_cast<int>(std::max<long>(parts, 1));
 }
@@ -380,7 +464,11 @@ Error launch_csr(CsrRole role, const CSR& A, const float* B, float* C, int N,
 
     EngineOpts o = opts ? *opts : EngineOpts{};
     int want_vec = o.vec;
-    if (role == CsrRole::Tiled && want_vec == 0) want_vec = 1;
+    int want_groups = o.groups;
+    if (role == CsrRole::Tiled && want_vec == 0) {
+        want_vec = 1;  // one lane per column, 64 columns per pass
+        if (want_groups == 0) want_groups = 1;
+    }
     if ((role == CsrRole::TiledV2 || role == CsrRole::TiledV4) && want_vec == 0) want_vec = 4;
     if (role == CsrRole::TiledV2) {
         if (N % 128 != 0) {
@@ -395,8 +483,12 @@ Error launch_csr(CsrRole role, const CSR& A, const float* B, float* C, int N,
         return fail(kInvalid, "engine vec must be 1, 2 or 4");
     }
     const int vec = pick_vec(N, B, C, want_vec);
-    const int waves = o.waves == 8 ? 8 : 4;
-    const int unroll = o.unroll == 8 ? 8 : 16;
+    const int groups = pick_groups(N, vec, want_groups);
+    // Defaults measured on MI355X (c1 / c2 / c5 sweeps): 8 waves per
+    // workgroup, 8 row segments in flight per lane, about 80 nonzeros per wave
+    // and at least 512 workgroups (two per CU) when the matrix allows it.
+    const int waves = (o.waves == 2 || o.waves == 4) ? o.waves : 8;
+    const int unroll = o.unroll == 16 ? 16 : 8;
 
     RowblockArgs args{A.row_ptr, A.col_idx, A.values, B, C, bounds, M, N, 0};
     int grid = 0;
@@ -405,9 +497,9 @@ Error launch_csr(CsrRole role, const CSR& A, const float* B, float* C, int N,
     } else {
         int rpb = o.rows_per_block;
         if (rpb <= 0) {
-            // About 128 nonzeros per wave on average.
             const double avg = A.nnz > 0 ? static_cast<double>(A.nnz) / M : 1.0;
-            rpb = static_cast<int>(128.0 * waves / std::max(avg, 1.0) + 0.5);
+            rpb = static_cast<int>(80.0 * waves / std::max(avg, 1.0) + 0.5);
+            rpb = std::min(rpb, M / 512);
         }
         rpb = std::max(1, std::min(rpb, kRpCap));
         args.rows_per_block = rpb;
@@ -415,11 +507,11 @@ Error launch_csr(CsrRole role, const CSR& A, const float* B, float* C, int N,
     }
     hipError_t e;
     if (vec == 4) {
-        e = dispatch_waves_unroll<4>(waves, unroll, args, grid, stream);
+        e = dispatch_groups<4>(groups, waves, unroll, args, grid, stream);
     } else if (vec == 2) {
-        e = dispatch_waves_unroll<2>(waves, unroll, args, grid, stream);
+        e = dispatch_groups<2>(groups, waves, unroll, args, grid, stream);
     } else {
-        e = dispatch_waves_unroll<1>(waves, unroll, args, grid, stream);
+        e = dispatch_groups<1>(groups, waves, unroll, args, grid, stream);
     }
     return from_hip(e, "csr engine launch");
 }

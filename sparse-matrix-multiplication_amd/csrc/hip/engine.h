@@ -36,9 +36,10 @@ enum class CsrRole : int {
 // Tuning of the row-block engine.  Zero fields mean "choose automatically".
 struct EngineOpts {
     int vec            = 0;  // floats per lane per B load: 1, 2 or 4
-    int waves          = 0;  // waves per workgroup: 4 or 8
-    int unroll         = 0;  // B-row loads in flight per wave: 8 or 16
+    int waves          = 0;  // waves per workgroup: 2, 4 or 8
+    int unroll         = 0;  // B-row loads in flight per lane per step: 8 or 16
     int rows_per_block = 0;  // implicit partition: rows per workgroup
+    int groups         = 0;  // lane groups per wave (entries interleaved): 1, 2 or 4
 };
 
 struct Error {

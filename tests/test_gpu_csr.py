@@ -133,13 +133,13 @@ def test_engine_deterministic(S, torch, config_refs):
 
 
 @pytest.mark.parametrize("vec", [1, 2, 4])
-@pytest.mark.parametrize("waves", [4, 8])
-@pytest.mark.parametrize("unroll", [8, 16])
-def test_engine_variants(S, torch, edge_cases, config_refs, vec, waves, unroll):
-    opts = S.EngineOptsT(vec, waves, unroll, 0)
-    for name in ("ragged", "power_law_small", "n96", "n257", "n512", "empty_nnz"):
+@pytest.mark.parametrize("groups", [1, 2, 4])
+@pytest.mark.parametrize("waves,unroll", [(2, 16), (4, 8), (8, 16)])
+def test_engine_variants(S, torch, edge_cases, config_refs, vec, groups, waves, unroll):
+    opts = S.EngineOptsT(vec, waves, unroll, 0, groups)
+    for name in ("ragged", "power_law_small", "n3", "n17", "n96", "n257", "n512", "empty_nnz"):
         A, B, C64, absC = edge_cases[name]
-        say(f"csr engine vec={vec} waves={waves} unroll={unroll} case={name}")
+        say(f"csr engine vec={vec} groups={groups} waves={waves} unroll={unroll} case={name}")
         dA = S.DeviceCSR(A)
         dB = torch.from_numpy(B).cuda()
         dC = torch.full((A.num_rows, B.shape[1]), float("nan"), device="cuda")
@@ -148,11 +148,11 @@ def test_engine_variants(S, torch, edge_cases, config_refs, vec, waves, unroll):
         check_csr(dC.cpu().numpy(), C64, absC)
     for rpb in (1, 7, 1024):
         A, B, C64, absC = edge_cases["ragged"]
-        say(f"csr engine vec={vec} waves={waves} unroll={unroll} rows_per_block={rpb}")
+        say(f"csr engine vec={vec} groups={groups} waves={waves} unroll={unroll} rows_per_block={rpb}")
         dA = S.DeviceCSR(A)
         dB = torch.from_numpy(B).cuda()
         dC = torch.full((A.num_rows, B.shape[1]), float("nan"), device="cuda")
-        S.spmm_tiled_v3_opts(dA, dB, S.EngineOptsT(vec, waves, unroll, rpb), dC)
+        S.spmm_tiled_v3_opts(dA, dB, S.EngineOptsT(vec, waves, unroll, rpb, groups), dC)
         torch.cuda.synchronize()
         check_csr(dC.cpu().numpy(), C64, absC)
 

@@ -88,7 +88,16 @@ typedef struct spmm_engine_opts_t {
     int unroll;         /* B row segments in flight per lane per step: 8, 16 */
     int rows_per_block; /* implicit partition granularity */
     int groups;         /* lane groups per wave, entries interleaved: 1, 2, 4 */
+    int slices;         /* XCD-tied column slices of B and C: 1, 2, 4, 8 */
 } spmm_engine_opts_t;
+
+/* BSR matrix-core kernel tuning (0 = automatic).  No counterpart in the
+ * reference: exposes the kernel's variants for measurement sweeps. */
+typedef struct spmm_bsr_opts_t {
+    int row_group; /* block-rows per workgroup sharing staged B tiles: 4, 8 */
+    int tiles;     /* 16-column MFMA tiles per workgroup: 1, 2, 4, 8 */
+    int per_wave;  /* 1: one independent wave per block-row, no B sharing */
+} spmm_bsr_opts_t;
 
 const char* spmm_c_last_error(void);
 const char* spmm_c_version(void);
@@ -164,6 +173,9 @@ int spmm_c_float_to_half(const float* d_src, uint16_t* d_dst, long n_elements,
                          void* stream);                          /* spmm_wmma.h:32 */
 int spmm_c_wmma(const spmm_bsr_t* d_bsr, const uint16_t* d_B_fp16, float* d_C, int N,
                 void* stream);                                   /* spmm_wmma.h:39 */
+/* spmm_wmma with explicit kernel options (no reference counterpart). */
+int spmm_c_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B_fp16, float* d_C, int N,
+                     const spmm_bsr_opts_t* opts, void* stream);
 
 /* ---- hybrid dispatch (spmm_hybrid.h:48-64) ---------------------------- */
 float spmm_c_hybrid_default_threshold(void);
@@ -185,6 +197,10 @@ int spmm_c_launch_repeat(int kernel_id, const void* d_A_any, const void* d_B, fl
 /* Same with explicit engine options for kernel id 5 (tiled_v3). */
 int spmm_c_launch_repeat_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
                               const spmm_engine_opts_t* opts, int reps, void* stream);
+/* Same for the matrix-core kernel with explicit options. */
+int spmm_c_launch_repeat_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B_fp16,
+                                   float* d_C, int N, const spmm_bsr_opts_t* opts, int reps,
+                                   void* stream);
 /* Times `reps` back-to-back launches between two hipEvents recorded on
  * `stream`; writes the elapsed milliseconds of the whole batch. */
 int spmm_c_time_repeat(int kernel_id, const void* d_A_any, const void* d_B, float* d_C,

@@ -69,6 +69,7 @@ struct BsrArgs {
     int             N;
     int             block_rows;
     int             b_vec_ok;  // N % 8 == 0 and B 16-byte aligned
+    int             block_cols;
 };
 
 // One wave = one block-row x (16*J) columns.  Workgroup = 4 independent waves
@@ -160,6 +161,216 @@ __global__ __launch_bounds__(256) void bsr_mfma_kernel(BsrArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Row-group kernel (the default path).
+//
+// A workgroup of RG waves owns RG consecutive block-rows (one per wave) and
+// a tile of NT = 16*J columns.  It first ORs the block-columns of its
+// block-rows into an LDS bitmap, then walks that union in ascending pairs
+// (bc0, bc1): each pair's 32 B rows x NT columns are loaded once into LDS,
+// row-major, with 16-byte loads, and every wave that owns a block at bc0 or
+// bc1 multiplies it by the staged rows.  Block-rows with shared block-columns
+// (banded, block-diagonal) therefore read each B tile once per workgroup
+// instead of once per block-row.
+//
+// The B operand is read back with ds_read_b64_tr_b16, which returns the
+// transpose of a 4 (k) x 16 (n) fp16 tile to each 16-lane block: lane s of the
+// block addresses row 8g + s/4 (+4 for the second read), columns 4*(s%4) ..
+// +3, and lane t receives rows 8g .. 8g+3 (8g+4 .. 8g+7) of column t, i.e. the
+// K-contiguous B operand of v_mfma_f32_16x16x32_f16.
+//
+// Pairs are processed in batches of P: all B tiles and A operands of a batch
+// are requested into registers before any is used, then stored to P LDS
+// tiles, so a batch costs one memory latency instead of one per pair.
+// ---------------------------------------------------------------------------
+constexpr int kMaxUnionWords = 2048;  // union bitmap of up to 65536 block-columns
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ s16x4 lds_read_tr16(const _Float16* p) {
+    // generic -> LDS address-space cast; p always points into a __shared__ array
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(const_cast<_Float16*>(p)));
+}
+
+template <int RG, int J, int P>
+__global__ __launch_bounds__(RG * 64) void bsr_rowgroup_kernel(BsrArgs a) {
+    constexpr int NT          = 16 * J;      // columns per workgroup
+    constexpr int S           = NT + 16;     // LDS row stride in fp16: S/2 = 8 (mod 32) banks
+    constexpr int CH          = NT / 8;      // 16-byte chunks per staged row
+    constexpr int TILE_CHUNKS = 32 * CH;
+    constexpr int THREADS     = RG * 64;
+    constexpr int CPT         = (TILE_CHUNKS + THREADS - 1) / THREADS;  // chunks per thread
+
+    __shared__ uint32_t s_bits[kMaxUnionWords];
+    __shared__ __attribute__((aligned(16))) _Float16 s_b[P][32 * S];  // one tile per pair of a batch
+
+    const int tid    = threadIdx.x;
+    const int lane   = tid & 63;
+    const int wave   = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g      = lane >> 4;
+    const int t      = lane & 15;
+    const int br     = blockIdx.x * RG + wave;
+    const int n0     = blockIdx.y * NT;
+    const int nwords = (a.block_cols + 31) / 32;
+
+    // ---- union of the group's block-columns
+    for (int i = tid; i < nwords; i += THREADS) s_bits[i] = 0u;
+    __syncthreads();
+    int bs = 0, be = 0;
+    if (br < a.block_rows) {
+        bs = a.row_ptr[br];
+        be = a.row_ptr[br + 1];
+    }
+    for (int b = bs + lane; b < be; b += 64) {
+        const int bc = a.col_idx[b];
+        if (static_cast<unsigned>(bc) < static_cast<unsigned>(a.block_cols)) {
+            atomicOr(&s_bits[bc >> 5], 1u << (bc & 31));
+        }
+    }
+    __syncthreads();
+
+    // ---- this wave's own block list (64 block-columns per register chunk)
+    int ptr = bs, chunk = bs;
+    int my_col = (bs + lane < be) ? a.col_idx[bs + lane] : 0x7fffffff;
+    auto current_col = [&]() -> int {
+        if (ptr >= be) return 0x7fffffff;
+        if (ptr - chunk >= 64) {
+            chunk = ptr;
+            my_col = (ptr + lane < be) ? a.col_idx[ptr + lane] : 0x7fffffff;
+        }
+        return __builtin_amdgcn_readlane(my_col, ptr - chunk);
+    };
+
+    // ---- cursor over the union (identical in every thread)
+    int cw = -1;
+    uint32_t cbits = 0u;
+    auto next_col = [&]() -> int {
+        while (cbits == 0u) {
+            if (++cw >= nwords) return -1;
+            cbits = s_bits[cw];
+        }
+        const int b = __builtin_ctz(cbits);
+        cbits &= cbits - 1u;
+        return cw * 32 + b;
+    };
+
+    auto load_tile = [&](int bc0, int bc1, f16x8 (&r)[CPT]) {
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int idx = tid + c * THREADS;
+            f16x8 v = f16x8(static_cast<_Float16>(0.0f));
+            if (idx < TILE_CHUNKS) {
+                const int s  = idx / CH;
+                const int bc = s < 16 ? bc0 : bc1;
+                const int k  = bc * 16 + (s & 15);
+                const int n  = n0 + (idx % CH) * 8;
+                if (bc >= 0 && k < a.K && n < a.N) {
+                    const _Float16* src = a.B + static_cast<size_t>(k) * a.N + n;
+                    if (a.b_vec_ok && n + 8 <= a.N) {
+                        v = *reinterpret_cast<const f16x8*>(src);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            if (n + e < a.N) v[e] = src[e];
+                        }
+                    }
+                }
+            }
+            r[c] = v;
+        }
+    };
+    auto store_tile = [&](int buf, const f16x8 (&r)[CPT]) {
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int idx = tid + c * THREADS;
+            if (idx < TILE_CHUNKS) {
+                *reinterpret_cast<f16x8*>(&s_b[buf][(idx / CH) * S + (idx % CH) * 8]) = r[c];
+            }
+        }
+    };
+    // A operand of this wave for the pair; consumes the wave's matching blocks.
+    auto load_a = [&](int bc0, int bc1, bool& any) -> f16x8 {
+        int blk0 = -1, blk1 = -1;
+        if (current_col() == bc0) blk0 = ptr++;
+        if (bc1 >= 0 && current_col() == bc1) blk1 = ptr++;
+        any = blk0 >= 0 || blk1 >= 0;
+        const int blk = g < 2 ? blk0 : blk1;
+        f16x8 af = f16x8(static_cast<_Float16>(0.0f));
+        if (blk >= 0) {
+            af = *reinterpret_cast<const f16x8*>(a.vals + static_cast<size_t>(blk) * 256 + t * 16 +
+                                                 8 * (g & 1));
+        }
+        return af;
+    };
+
+    f32x4 acc[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) acc[j] = f32x4(0.0f);
+
+    // Batches of up to P pairs: every B tile and A operand of a batch is
+    // requested before any is used, so a batch costs one memory latency.
+    while (true) {
+        int bcl[2 * P];
+        int npairs = 0;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            bcl[2 * p]     = next_col();
+            bcl[2 * p + 1] = bcl[2 * p] >= 0 ? next_col() : -1;
+            npairs += bcl[2 * p] >= 0 ? 1 : 0;
+        }
+        if (npairs == 0) break;  // uniform across the workgroup
+
+        f16x8 treg[P][CPT];
+        f16x8 af[P];
+        bool  any[P];
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            any[p] = false;
+            af[p]  = f16x8(static_cast<_Float16>(0.0f));
+            if (p < npairs) {
+                load_tile(bcl[2 * p], bcl[2 * p + 1], treg[p]);
+                af[p] = load_a(bcl[2 * p], bcl[2 * p + 1], any[p]);
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            if (p < npairs) store_tile(p, treg[p]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            if (p < npairs && any[p]) {
+                const _Float16* rowp = &s_b[p][(8 * g + (t >> 2)) * S + 4 * (t & 3)];
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    const s16x4 lo = lds_read_tr16(rowp + 16 * j);
+                    const s16x4 hi = lds_read_tr16(rowp + 4 * S + 16 * j);
+                    const s16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        af[p], __builtin_bit_cast(f16x8, both), acc[j], 0, 0, 0);
+                }
+            }
+        }
+        if (npairs < P) break;
+        __syncthreads();  // the next batch overwrites the tiles
+    }
+
+    if (br < a.block_rows) {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int col = n0 + 16 * j + t;
+            if (col >= a.N) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = br * 16 + 4 * g + i;
+                if (row < a.M) a.C[static_cast<size_t>(row) * a.N + col] = acc[j][i];
+            }
+        }
+    }
+}
+
 Error fail(int status, std::string msg) { return Error{status, std::move(msg)}; }
 
 Error from_hip(hipError_t e, const char* what) {
@@ -172,6 +383,26 @@ hipError_t run_bsr(const BsrArgs& args, hipStream_t stream) {
     dim3 grid(ceil_div(args.block_rows, 4), ceil_div(args.N, 16 * J));
     hipLaunchKernelGGL((bsr_mfma_kernel<J>), grid, dim3(256), 0, stream, args);
     return hipGetLastError();
+}
+
+template <int RG, int J>
+hipError_t run_rowgroup(const BsrArgs& args, hipStream_t stream) {
+    dim3 grid(ceil_div(args.block_rows, RG), ceil_div(args.N, 16 * J));
+    // batch of 8 pairs (16 block-columns): one diagonal block of c4, a whole
+    // banded row group of c3; wide tiles take 4 to bound LDS and registers
+    constexpr int P = J >= 8 ? 4 : 8;
+    hipLaunchKernelGGL((bsr_rowgroup_kernel<RG, J, P>), grid, dim3(RG * 64), 0, stream, args);
+    return hipGetLastError();
+}
+
+template <int RG>
+hipError_t dispatch_rowgroup(int j, const BsrArgs& args, hipStream_t stream) {
+    switch (j) {
+        case 1: return run_rowgroup<RG, 1>(args, stream);
+        case 2: return run_rowgroup<RG, 2>(args, stream);
+        case 8: return run_rowgroup<RG, 8>(args, stream);
+        default: return run_rowgroup<RG, 4>(args, stream);
+    }
 }
 
 }  // namespace
@@ -190,7 +421,8 @@ Error launch_float_to_half(const float* src, half* dst, long n, hipStream_t stre
     return from_hip(hipGetLastError(), "float_to_half launch");
 }
 
-Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t stream) {
+Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t stream,
+                 const BsrOpts* opts) {
     if (A.num_rows < 0 || A.num_cols < 0 || A.num_blocks < 0 || N < 0) {
         return fail(kInvalid, "negative matrix dimension");
     }
@@ -216,14 +448,23 @@ Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t strea
                  A.num_cols,
                  N,
                  A.block_rows,
-                 (N % 8 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0) ? 1 : 0};
+                 (N % 8 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0) ? 1 : 0,
+                 A.block_cols};
+    const BsrOpts o = opts ? *opts : BsrOpts{};
+    int j = o.tiles;
+    if (j != 1 && j != 2 && j != 4 && j != 8) j = N <= 16 ? 1 : (N <= 32 ? 2 : 4);
     hipError_t e;
-    if (N <= 16) {
-        e = run_bsr<1>(args, stream);
-    } else if (N <= 32) {
-        e = run_bsr<2>(args, stream);
+    const int nwords = (A.block_cols + 31) / 32;
+    if (o.per_wave || nwords > kMaxUnionWords) {
+        // one wave per block-row, no sharing of B tiles (also the path for
+        // K beyond the union bitmap's 65536 block-columns)
+        const int jj = j > 4 ? 4 : j;
+        e = jj == 1 ? run_bsr<1>(args, stream) : (jj == 2 ? run_bsr<2>(args, stream)
+                                                          : run_bsr<4>(args, stream));
+    } else if (o.row_group == 8) {
+        e = dispatch_rowgroup<8>(j, args, stream);
     } else {
-        e = run_bsr<4>(args, stream);
+        e = dispatch_rowgroup<4>(j, args, stream);
     }
     return from_hip(e, "spmm_wmma launch");
 }

@@ -148,6 +148,7 @@ spmm::engine::EngineOpts opts_from_c(const spmm_engine_opts_t* o) {
         e.unroll         = o->unroll;
         e.rows_per_block = o->rows_per_block;
         e.groups         = o->groups;
+        e.slices         = o->slices;
     }
     return e;
 }
@@ -497,6 +498,29 @@ int spmm_c_float_to_half(const float* d_src, uint16_t* d_dst, long n, void* stre
 int spmm_c_wmma(const spmm_bsr_t* d_bsr, const uint16_t* d_B16, float* d_C, int N,
                 void* stream) {
     return launch_id(7, d_bsr, d_B16, d_C, N, stream);
+}
+
+int spmm_c_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B16, float* d_C, int N,
+                     const spmm_bsr_opts_t* opts, void* stream) {
+    if (d_bsr == nullptr) return set_error(SPMM_INVALID, "null matrix descriptor");
+    spmm::engine::BsrOpts o;
+    if (opts != nullptr) {
+        o.row_group = opts->row_group;
+        o.tiles     = opts->tiles;
+        o.per_wave  = opts->per_wave;
+    }
+    return from_engine(spmm::engine::launch_bsr(to_cpp(*d_bsr),
+                                                reinterpret_cast<const half*>(d_B16), d_C, N,
+                                                as_stream(stream), &o));
+}
+
+int spmm_c_launch_repeat_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B16, float* d_C,
+                                   int N, const spmm_bsr_opts_t* opts, int reps, void* stream) {
+    for (int i = 0; i < reps; ++i) {
+        const int rc = spmm_c_wmma_opts(d_bsr, d_B16, d_C, N, opts, stream);
+        if (rc != SPMM_OK) return rc;
+    }
+    return ok();
 }
 
 // ---- hybrid ------------------------------------------------------------------

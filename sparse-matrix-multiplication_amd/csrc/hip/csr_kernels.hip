@@ -136,6 +136,9 @@ struct RowblockArgs {
     int          M;
     int          N;
     int          rows_per_block;
+    int          nblocks;      // row blocks (workgroups of one column slice)
+    int          slices;       // column slices: 1, 2, 4 or 8
+    int          slice_cols;   // columns per slice (a multiple of VEC)
 };
 
 constexpr int kRpCap = 1024;
@@ -199,12 +202,27 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
     const int glane = lane % LPG;
     const int N     = a.N;
 
+    // Column slices are tied to XCDs: workgroups are dispatched round-robin
+    // over the 8 XCDs, so workgroup g runs on XCD g % 8.  With S slices, XCDs
+    // s*8/S .. (s+1)*8/S - 1 compute columns [s*SC, (s+1)*SC) of every row
+    // block, so each XCD's L2 holds only 1/S of B.
+    int rb = blockIdx.x, slice = 0;
+    if (a.slices > 1) {
+        const int per = 8 / a.slices;  // XCDs per slice
+        const int x   = blockIdx.x & 7;
+        rb    = (blockIdx.x >> 3) * per + x % per;
+        slice = x / per;
+    }
+    if (rb >= a.nblocks) return;  // whole workgroup, before any barrier
+    const int cbeg = slice * a.slice_cols;
+    const int cend = min(N, cbeg + a.slice_cols);
+
     int r_begin, r_end;
     if (a.bounds != nullptr) {
-        r_begin = a.bounds[blockIdx.x];
-        r_end   = a.bounds[blockIdx.x + 1];
+        r_begin = a.bounds[rb];
+        r_end   = a.bounds[rb + 1];
     } else {
-        r_begin = blockIdx.x * a.rows_per_block;
+        r_begin = rb * a.rows_per_block;
         r_end   = min(a.M, r_begin + a.rows_per_block);
     }
 
@@ -222,7 +240,9 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
                 const int b = __builtin_ctzll(empty);
                 empty &= empty - 1;
                 float* crow = a.C + static_cast<size_t>(w0 + base + b) * N;
-                for (int c = lane * VEC; c < N; c += kWave * VEC) store_vec<VEC>(crow + c, vzero<VEC>());
+                for (int c = cbeg + lane * VEC; c < cend; c += kWave * VEC) {
+                    store_vec<VEC>(crow + c, vzero<VEC>());
+                }
             }
         }
 
@@ -243,9 +263,9 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
             first = lo;
         }
 
-        for (int c0 = 0; c0 < N; c0 += COLS) {
+        for (int c0 = cbeg; c0 < cend; c0 += COLS) {
             const int  col    = c0 + glane * VEC;
-            const bool col_ok = col < N;
+            const bool col_ok = col < cend;
             const int  col_ld = col_ok ? col : 0;  // loads stay in bounds; never stored
             const bool writer = grp == 0 && col_ok;
             if (lane == 0) s_first[wave] = (pa < pb) ? -1 : -2;
@@ -483,17 +503,22 @@ Error launch_csr(CsrRole role, const CSR& A, const float* B, float* C, int N,
         return fail(kInvalid, "engine vec must be 1, 2 or 4");
     }
     const int vec = pick_vec(N, B, C, want_vec);
-    const int groups = pick_groups(N, vec, want_groups);
+    // Column slices (XCD-aware, see the kernel): 1, 2, 4 or 8.
+    int slices = o.slices;
+    if (slices != 1 && slices != 2 && slices != 4 && slices != 8) slices = 1;
+    int slice_cols = ceil_div(N, slices);
+    slice_cols = ceil_div(slice_cols, vec) * vec;
+    const int groups = pick_groups(slice_cols, vec, want_groups);
     // Defaults measured on MI355X (c1 / c2 / c5 sweeps): 8 waves per
     // workgroup, 8 row segments in flight per lane, about 80 nonzeros per wave
     // and at least 512 workgroups (two per CU) when the matrix allows it.
     const int waves = (o.waves == 2 || o.waves == 4) ? o.waves : 8;
     const int unroll = o.unroll == 16 ? 16 : 8;
 
-    RowblockArgs args{A.row_ptr, A.col_idx, A.values, B, C, bounds, M, N, 0};
-    int grid = 0;
+    RowblockArgs args{A.row_ptr, A.col_idx, A.values, B, C, bounds, M, N, 0, 0, slices,
+                      slice_cols};
     if (bounds != nullptr) {
-        grid = parts;
+        args.nblocks = parts;
     } else {
         int rpb = o.rows_per_block;
         if (rpb <= 0) {
@@ -503,8 +528,9 @@ Error launch_csr(CsrRole role, const CSR& A, const float* B, float* C, int N,
         }
         rpb = std::max(1, std::min(rpb, kRpCap));
         args.rows_per_block = rpb;
-        grid = ceil_div(M, rpb);
+        args.nblocks = ceil_div(M, rpb);
     }
+    const int grid = slices == 1 ? args.nblocks : ceil_div(args.nblocks, 8 / slices) * 8;
     hipError_t e;
     if (vec == 4) {
         e = dispatch_groups<4>(groups, waves, unroll, args, grid, stream);

@@ -40,6 +40,7 @@ struct EngineOpts {
     int unroll         = 0;  // B-row loads in flight per lane per step: 8 or 16
     int rows_per_block = 0;  // implicit partition: rows per workgroup
     int groups         = 0;  // lane groups per wave (entries interleaved): 1, 2 or 4
+    int slices         = 0;  // XCD-tied column slices of B and C: 1, 2, 4 or 8
 };
 
 struct Error {
@@ -55,7 +56,15 @@ Error launch_csr(CsrRole role, const CSR& d_A, const float* d_B, float* d_C, int
 
 Error launch_float_to_half(const float* d_src, half* d_dst, long n, hipStream_t stream);
 
-Error launch_bsr(const BSR& d_A, const half* d_B, float* d_C, int N, hipStream_t stream);
+// Tuning of the BSR matrix-core kernel.  Zero fields mean "choose automatically".
+struct BsrOpts {
+    int row_group = 0;  // block-rows (waves) per workgroup sharing B tiles: 4 or 8
+    int tiles     = 0;  // 16-column MFMA tiles per workgroup: 1, 2, 4 or 8
+    int per_wave  = 0;  // 1: independent wave per block-row (no B sharing)
+};
+
+Error launch_bsr(const BSR& d_A, const half* d_B, float* d_C, int N, hipStream_t stream,
+                 const BsrOpts* opts = nullptr);
 
 // Number of workgroups the engine uses for an explicit partition of this CSR.
 int default_partition_parts(int num_rows, int nnz);

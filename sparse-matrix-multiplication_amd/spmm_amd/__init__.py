@@ -66,7 +66,12 @@ class HybridPlanT(ctypes.Structure):
 
 class EngineOptsT(ctypes.Structure):
     _fields_ = [("vec", ctypes.c_int), ("waves", ctypes.c_int), ("unroll", ctypes.c_int),
-                ("rows_per_block", ctypes.c_int), ("groups", ctypes.c_int)]
+                ("rows_per_block", ctypes.c_int), ("groups", ctypes.c_int),
+                ("slices", ctypes.c_int)]
+
+
+class BsrOptsT(ctypes.Structure):
+    _fields_ = [("row_group", ctypes.c_int), ("tiles", ctypes.c_int), ("per_wave", ctypes.c_int)]
 
 
 _P = ctypes.POINTER
@@ -112,6 +117,8 @@ _SIGNATURES = {
     "spmm_c_tiled_v3_opts": (_int, [_P(CsrT), _vp, _vp, _int, _P(EngineOptsT), _vp]),
     "spmm_c_float_to_half": (_int, [_vp, _vp, _long, _vp]),
     "spmm_c_wmma": (_int, [_P(BsrT), _vp, _vp, _int, _vp]),
+    "spmm_c_wmma_opts": (_int, [_P(BsrT), _vp, _vp, _int, _P(BsrOptsT), _vp]),
+    "spmm_c_launch_repeat_wmma_opts": (_int, [_P(BsrT), _vp, _vp, _int, _P(BsrOptsT), _int, _vp]),
     "spmm_c_hybrid_default_threshold": (_float, []),
     "spmm_c_hybrid_choose": (_int, [_P(CsrT), _int, _float, _P(HybridPlanT)]),
     "spmm_c_backend_name": (ctypes.c_char_p, [_int]),
@@ -530,6 +537,25 @@ def spmm_wmma(A: DeviceBSR, B16, C=None, stream=None):
     _check(lib().spmm_c_wmma(ctypes.byref(s), B16.data_ptr(), C.data_ptr(), N,
                              _stream_handle(stream)))
     return C
+
+
+def spmm_wmma_opts(A: DeviceBSR, B16, opts: BsrOptsT, C=None, stream=None):
+    """spmm_wmma with explicit kernel options (row group, column tiles, per-wave)."""
+    torch = _torch()
+    N = int(B16.shape[1])
+    if C is None:
+        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B16.device)
+    s = A.struct()
+    _check(lib().spmm_c_wmma_opts(ctypes.byref(s), B16.data_ptr(), C.data_ptr(), N,
+                                  ctypes.byref(opts), _stream_handle(stream)))
+    return C
+
+
+def launch_repeat_wmma_opts(A: DeviceBSR, B16, C, opts: BsrOptsT, reps: int, stream=None) -> None:
+    s = A.struct()
+    _check(lib().spmm_c_launch_repeat_wmma_opts(ctypes.byref(s), B16.data_ptr(), C.data_ptr(),
+                                                int(B16.shape[1]), ctypes.byref(opts), reps,
+                                                _stream_handle(stream)))
 
 
 def launch_repeat(kernel: str, A, B, C, reps: int, stream=None) -> None:

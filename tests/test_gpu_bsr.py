@@ -91,6 +91,42 @@ def test_wmma_cases(S, O, torch, name):
     check_csr(C, C64, absC, tol=1e-5)
 
 
+@pytest.mark.parametrize("row_group,tiles,per_wave", [(4, 1, 0), (4, 2, 0), (4, 4, 0), (4, 8, 0),
+                                                       (8, 1, 0), (8, 4, 0), (8, 8, 0),
+                                                       (0, 1, 1), (0, 2, 1), (0, 4, 1)])
+def test_wmma_variants(S, O, torch, row_group, tiles, per_wave):
+    cases = _cases(S)
+    for name in ("single_block", "odd_pair_count", "ragged_dims", "n_not_16", "n_1",
+                 "empty_block_rows", "empty", "wide_n", "block_diag_small"):
+        A, B = cases[name]
+        hb, B16, C32, C64, absC = _refs(S, O, A, B)
+        say(f"wmma opts row_group={row_group} tiles={tiles} per_wave={per_wave} case={name}")
+        dA = S.DeviceBSR(hb)
+        dB = torch.from_numpy(B16.view(np.int16)).cuda()
+        dC = torch.full((hb.num_rows, B16.shape[1]), float("nan"), device="cuda")
+        S.spmm_wmma_opts(dA, dB, S.BsrOptsT(row_group, tiles, per_wave), dC)
+        torch.cuda.synchronize()
+        C = dC.cpu().numpy()
+        check_bsr(C, C32, absC)
+        check_csr(C, C64, absC, tol=1e-5)
+
+
+def test_wmma_long_block_rows(S, O, torch):
+    # block-rows with more than 64 blocks (the per-wave register chunk) and a
+    # union wider than one bitmap word
+    A = S.generate_uniform_random_csr(64, 2048, 0.05, 31)
+    A.values = S.round_to_fp16(A.values)
+    B = S.round_to_fp16(np.random.default_rng(3).uniform(-1, 1, (2048, 64)).astype(np.float32))
+    hb, B16, C32, C64, absC = _refs(S, O, A, B)
+    assert np.diff(hb.row_ptr).max() > 64
+    for rg in (4, 8):
+        say(f"wmma long block-rows row_group={rg} blocks={hb.num_blocks}")
+        C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
+                             S.BsrOptsT(rg, 4, 0)).cpu().numpy()
+        check_bsr(C, C32, absC)
+        check_csr(C, C64, absC, tol=1e-5)
+
+
 @pytest.mark.parametrize("cfg", ["c3", "c4"])
 def test_wmma_configs(S, O, torch, cfg):
     A, B = make_config(S, cfg)

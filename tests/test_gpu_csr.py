@@ -157,6 +157,28 @@ def test_engine_variants(S, torch, edge_cases, config_refs, vec, groups, waves, 
         check_csr(dC.cpu().numpy(), C64, absC)
 
 
+@pytest.mark.parametrize("slices", [2, 4, 8])
+@pytest.mark.parametrize("vec", [0, 1])
+def test_engine_column_slices(S, torch, edge_cases, config_refs, slices, vec):
+    opts = S.EngineOptsT(vec, 8, 8, 0, 0, slices)
+    for name in ("ragged", "power_law_small", "n1", "n3", "n17", "n96", "n130", "n257", "n512",
+                 "empty_nnz", "identity"):
+        A, B, C64, absC = edge_cases[name]
+        say(f"csr engine slices={slices} vec={vec} case={name}")
+        dA = S.DeviceCSR(A)
+        dB = torch.from_numpy(B).cuda()
+        dC = torch.full((A.num_rows, B.shape[1]), float("nan"), device="cuda")
+        S.spmm_tiled_v3_opts(dA, dB, opts, dC)
+        torch.cuda.synchronize()
+        check_csr(dC.cpu().numpy(), C64, absC)
+    A, B, C64, absC = config_refs("c5")
+    say(f"csr engine slices={slices} vec={vec} config=c5")
+    dC = torch.full((A.num_rows, B.shape[1]), float("nan"), device="cuda")
+    S.spmm_tiled_v3_opts(S.DeviceCSR(A), torch.from_numpy(B).cuda(), opts, dC)
+    torch.cuda.synchronize()
+    check_csr(dC.cpu().numpy(), C64, absC)
+
+
 @pytest.mark.parametrize("parts", [1, 3, 64, 5000])
 def test_partitioned_engine(S, torch, edge_cases, config_refs, parts):
     cases = [edge_cases["ragged"], edge_cases["power_law_small"], config_refs("c5")]

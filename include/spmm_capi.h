@@ -94,9 +94,11 @@ typedef struct spmm_engine_opts_t {
 /* BSR matrix-core kernel tuning (0 = automatic).  No counterpart in the
  * reference: exposes the kernel's variants for measurement sweeps. */
 typedef struct spmm_bsr_opts_t {
-    int row_group; /* block-rows per workgroup sharing staged B tiles: 4, 8 */
-    int tiles;     /* 16-column MFMA tiles per workgroup: 1, 2, 4, 8 */
-    int per_wave;  /* 1: one independent wave per block-row, no B sharing */
+    int row_group; /* 0: wave kernel (default); 1, 2, 4, 8: block-rows per
+                      workgroup sharing staged B tiles */
+    int tiles;     /* 16-column MFMA tiles per wave: 1, 2, 4 (8 with row groups) */
+    int per_wave;  /* 1: wave kernel whatever row_group says */
+    int depth;     /* wave kernel: block pairs in flight per wave: 1, 2, 4 */
 } spmm_bsr_opts_t;
 
 const char* spmm_c_last_error(void);

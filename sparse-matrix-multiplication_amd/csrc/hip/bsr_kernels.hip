@@ -72,80 +72,155 @@ struct BsrArgs {
     int             block_cols;
 };
 
-// One wave = one block-row x (16*J) columns.  Workgroup = 4 independent waves
-// on 4 consecutive block-rows (same column tile).
-template <int J>
-__global__ __launch_bounds__(256) void bsr_mfma_kernel(BsrArgs a) {
-    constexpr int WN     = 16 * J;   // columns per wave
-    constexpr int STRIDE = WN + 2;   // LDS row stride in fp16 (pad against bank conflicts)
-    constexpr int CHUNKS = WN / 8;   // 16-byte chunks per staged row
-    __shared__ _Float16 s_b[4][32 * STRIDE];
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+
+// ds_read_b64_tr_b16.  Within each 16-lane block, lane s supplies the address
+// of 4 consecutive fp16 values and output lane i receives element i % 4 of
+// the values addressed by lanes 4e + i/4, e = 0..3: with lane s pointing at
+// row s/4, columns 4*(s%4) .. +3 of a row-major [k][n] tile, lane i gets
+// rows 0..3 of column i -- a K-contiguous MFMA B operand.
+__device__ __forceinline__ s16x4 lds_read_tr16(const _Float16* p) {
+    // generic -> LDS address-space cast; p always points into a __shared__ array
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(const_cast<_Float16*>(p)));
+}
+
+// ---------------------------------------------------------------------------
+// Wave kernel (the default path): one wave = one block-row x 16*J columns,
+// four independent waves per workgroup, no workgroup barriers.  Maximum
+// parallelism and a small LDS footprint (one 32 x (16J+16) fp16 tile per
+// wave) keep many waves resident, which is what hides the latency of the
+// short dependent chain row_ptr -> col_idx -> (A, B) -> MFMA.
+//   - The block-row's block-columns come in with one vector load (lane i
+//     holds col_idx[first + i], 64 per chunk) and are broadcast with
+//     v_readlane, so pairs need no further index loads.
+//   - The A operands and B rows of the next D pairs are in flight while a
+//     pair is multiplied (a ring of D register sets).
+//   - B rows are written to the wave's LDS tile row-major (16-byte stores) and
+//     read back as MFMA operands with ds_read_b64_tr_b16 (two per operand).
+// LDS accesses of one wave execute in program order, so the single tile
+// needs no barrier between a pair's reads and the next pair's writes.
+// ---------------------------------------------------------------------------
+template <int J, int D, bool VEC>
+__global__ __launch_bounds__(256) void bsr_wave_kernel(BsrArgs a) {
+    constexpr int NT  = 16 * J;          // columns per wave
+    constexpr int S   = NT + 16;         // LDS row stride in fp16 (S/2 = 8 mod 32 banks)
+    constexpr int CH  = NT / 8;          // 16-byte chunks per staged row
+    constexpr int CPL = 32 * CH / 64;    // chunks per lane (J for the 32-row tile)
+    __shared__ __attribute__((aligned(16))) _Float16 s_b[4][32 * S];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g    = lane >> 4;
     const int t    = lane & 15;
     const int br   = blockIdx.x * 4 + wave;
-    const int n0   = blockIdx.y * WN;
-    if (br >= a.block_rows) return;  // no workgroup barrier below: waves are independent
-    _Float16* sb = s_b[wave];
+    const int n0   = blockIdx.y * NT;
+    if (br >= a.block_rows) return;  // waves are independent: no barrier anywhere
+    _Float16* tile = s_b[wave];
+
+    const int bs = a.row_ptr[br];
+    const int be = a.row_ptr[br + 1];
 
     f32x4 acc[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) acc[j] = f32x4(0.0f);
 
-    const int b_begin = a.row_ptr[br];
-    const int b_end   = a.row_ptr[br + 1];
-    for (int b = b_begin; b < b_end; b += 2) {
-        const bool pair = (b + 1) < b_end;
-        const int  bc0  = a.col_idx[b];
-        const int  bc1  = pair ? a.col_idx[b + 1] : 0;
-
-        // A operand: row t of block (g < 2 ? b : b+1), columns 8*(g&1) .. +7.
-        f16x8 af = f16x8(static_cast<_Float16>(0.0f));
-        if (g < 2 || pair) {
-            const int blk = g < 2 ? b : b + 1;
-            af = *reinterpret_cast<const f16x8*>(a.vals + static_cast<size_t>(blk) * 256 +
-                                                 t * 16 + 8 * (g & 1));
-        }
-
-        // Stage B rows: staged row s < 16 is K-row bc0*16 + s, s >= 16 is bc1*16 + s-16.
-        for (int idx = lane; idx < 32 * CHUNKS; idx += 64) {
-            const int s  = idx / CHUNKS;
-            const int ch = idx % CHUNKS;
-            const int k  = s < 16 ? bc0 * 16 + s : bc1 * 16 + (s - 16);
-            const int n  = n0 + ch * 8;
-            const bool row_ok = (s < 16 || pair) && static_cast<unsigned>(k) < static_cast<unsigned>(a.K);
-            f16x8 v = f16x8(static_cast<_Float16>(0.0f));
-            if (row_ok) {
-                const _Float16* src = a.B + static_cast<size_t>(k) * a.N + n;
-                if (a.b_vec_ok && n + 8 <= a.N) {
-                    v = *reinterpret_cast<const f16x8*>(src);
-                } else {
+    // Registers of one pair: this lane's B chunks and A operand, and which of
+    // them hold data.  Loads never branch: a lane whose row lies outside B
+    // (past K, or the absent second block of an odd tail) reads a clamped,
+    // valid address and its value is replaced by zero when it is used, so the
+    // loads of all pairs in flight stay independent of each other.
+    struct PairRegs {
+        f16x8 b[CPL];
+        f16x8 af;
+        bool  b_ok[CPL];
+        bool  a_ok;
+    };
+    // Pair = blocks base+p and base+p+1 of the row (p and p+1 inside the
+    // column-index chunk ci that starts at block base).
+    auto load_pair = [&](int base, int p, int cnt, int ci, PairRegs& r) {
+        const bool two = p + 1 < cnt;
+        const int bc0 = __builtin_amdgcn_readlane(ci, p);
+        const int bc1 = __builtin_amdgcn_readlane(ci, two ? p + 1 : p);
+        const int blk = base + p;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        if (n + e < a.N) v[e] = src[e];
-                    }
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = lane + c * 64;
+            const int s   = idx / CH;                 // staged row 0..31
+            const int k   = (s < 16 ? bc0 : bc1) * 16 + (s & 15);
+            const int n   = n0 + (idx % CH) * 8;
+            const bool ok = (s < 16 || two) && k < a.K && n < a.N;
+            r.b_ok[c] = ok;
+            if constexpr (VEC) {
+                const size_t off = ok ? static_cast<size_t>(k) * a.N + n : 0;
+                r.b[c] = *reinterpret_cast<const f16x8*>(a.B + off);
+            } else {
+                const size_t row = ok ? static_cast<size_t>(k) * a.N : 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const bool in = ok && n + e < a.N;
+                    const _Float16 x = a.B[in ? row + n + e : 0];
+                    r.b[c][e] = in ? x : static_cast<_Float16>(0.0f);
                 }
             }
-            f16x2* dst = reinterpret_cast<f16x2*>(sb + s * STRIDE + ch * 8);
-            dst[0] = f16x2{v[0], v[1]};
-            dst[1] = f16x2{v[2], v[3]};
-            dst[2] = f16x2{v[4], v[5]};
-            dst[3] = f16x2{v[6], v[7]};
         }
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
-        __builtin_amdgcn_wave_barrier();
-
+        // A operand: row t of block blk (g < 2) or blk+1 (g >= 2), columns 8*(g&1) .. +7
+        r.a_ok = g < 2 || two;
+        r.af = *reinterpret_cast<const f16x8*>(
+            a.vals + static_cast<size_t>(blk + (r.a_ok ? (g >> 1) : 0)) * 256 + t * 16 +
+            8 * (g & 1));
+    };
+    auto multiply = [&](const PairRegs& r) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = lane + c * 64;
+            const f16x8 zero = f16x8(static_cast<_Float16>(0.0f));
+            *reinterpret_cast<f16x8*>(&tile[(idx / CH) * S + (idx % CH) * 8]) =
+                r.b_ok[c] ? r.b[c] : zero;
+        }
+        const f16x8 af = r.a_ok ? r.af : f16x8(static_cast<_Float16>(0.0f));
+        const _Float16* rowp = &tile[(8 * g + (t >> 2)) * S + 4 * (t & 3)];
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            f16x8 bf;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) bf[i] = sb[(8 * g + i) * STRIDE + 16 * j + t];
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc[j], 0, 0, 0);
+            const s16x4 lo = lds_read_tr16(rowp + 16 * j);
+            const s16x4 hi = lds_read_tr16(rowp + 4 * S + 16 * j);
+            const s16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(f16x8, both),
+                                                             acc[j], 0, 0, 0);
         }
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // reads done before the next pair overwrites
-        __builtin_amdgcn_wave_barrier();
+    };
+
+    // D pairs in flight.  Pair i of a chunk lives in ring slot i % D.  The
+    // steady-state loop refills every slot it empties, so each slot's loads
+    // are issued unconditionally and the wait before a multiply covers only
+    // that slot's loads; the drain finishes the last (fewer than 2D) pairs.
+    for (int c0 = bs; c0 < be; c0 += 64) {  // 64 blocks per column-index chunk
+        const int cnt = min(64, be - c0);
+        const int np  = (cnt + 1) >> 1;     // pairs in this chunk
+        const int ci  = lane < cnt ? a.col_idx[c0 + lane] : 0;
+        PairRegs ring[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) load_pair(c0, 2 * min(d, np - 1), cnt, ci, ring[d]);
+        int i0 = 0;
+        for (; i0 + 2 * D <= np; i0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                multiply(ring[d]);
+                load_pair(c0, 2 * (i0 + d + D), cnt, ci, ring[d]);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (i0 + d < np) {
+                multiply(ring[d]);
+                if (i0 + d + D < np) load_pair(c0, 2 * (i0 + d + D), cnt, ci, ring[d]);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (i0 + D + d < np) multiply(ring[d]);
+        }
     }
 
     // D layout: lane holds rows 4*g + i, column t of each 16-column tile.
@@ -162,7 +237,7 @@ __global__ __launch_bounds__(256) void bsr_mfma_kernel(BsrArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Row-group kernel (the default path).
+// Row-group kernel.
 //
 // A workgroup of RG waves owns RG consecutive block-rows (one per wave) and
 // a tile of NT = 16*J columns.  It first ORs the block-columns of its
@@ -185,15 +260,6 @@ __global__ __launch_bounds__(256) void bsr_mfma_kernel(BsrArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int kMaxUnionWords = 2048;  // union bitmap of up to 65536 block-columns
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef short s16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ s16x4 lds_read_tr16(const _Float16* p) {
-    // generic -> LDS address-space cast; p always points into a __shared__ array
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4*)(const_cast<_Float16*>(p)));
-}
-
 template <int RG, int J, int P>
 __global__ __launch_bounds__(RG * 64) void bsr_rowgroup_kernel(BsrArgs a) {
     constexpr int NT          = 16 * J;      // columns per workgroup
@@ -203,8 +269,11 @@ __global__ __launch_bounds__(RG * 64) void bsr_rowgroup_kernel(BsrArgs a) {
     constexpr int THREADS     = RG * 64;
     constexpr int CPT         = (TILE_CHUNKS + THREADS - 1) / THREADS;  // chunks per thread
 
-    __shared__ uint32_t s_bits[kMaxUnionWords];
-    __shared__ __attribute__((aligned(16))) _Float16 s_b[P][32 * S];  // one tile per pair of a batch
+    // Dynamic LDS: P tiles of 32 x S fp16 (one per pair of a batch), then the
+    // union bitmap sized to the matrix's block-columns.
+    extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
+    _Float16 (*s_b)[32 * S] = reinterpret_cast<_Float16 (*)[32 * S]>(s_dyn);
+    uint32_t* s_bits = reinterpret_cast<uint32_t*>(s_dyn + sizeof(_Float16) * P * 32 * S);
 
     const int tid    = threadIdx.x;
     const int lane   = tid & 63;
@@ -215,25 +284,27 @@ __global__ __launch_bounds__(RG * 64) void bsr_rowgroup_kernel(BsrArgs a) {
     const int n0     = blockIdx.y * NT;
     const int nwords = (a.block_cols + 31) / 32;
 
-    // ---- union of the group's block-columns
-    for (int i = tid; i < nwords; i += THREADS) s_bits[i] = 0u;
-    __syncthreads();
     int bs = 0, be = 0;
     if (br < a.block_rows) {
         bs = a.row_ptr[br];
         be = a.row_ptr[br + 1];
     }
+    // this wave's own block list, 64 block-columns per register chunk; the
+    // first chunk also feeds the union below
+    int ptr = bs, chunk = bs;
+    int my_col = (bs + lane < be) ? a.col_idx[bs + lane] : 0x7fffffff;
+
+    // ---- union of the group's block-columns
+    for (int i = tid; i < nwords; i += THREADS) s_bits[i] = 0u;
+    __syncthreads();
     for (int b = bs + lane; b < be; b += 64) {
-        const int bc = a.col_idx[b];
+        const int bc = b - bs < 64 ? my_col : a.col_idx[b];
         if (static_cast<unsigned>(bc) < static_cast<unsigned>(a.block_cols)) {
             atomicOr(&s_bits[bc >> 5], 1u << (bc & 31));
         }
     }
     __syncthreads();
 
-    // ---- this wave's own block list (64 block-columns per register chunk)
-    int ptr = bs, chunk = bs;
-    int my_col = (bs + lane < be) ? a.col_idx[bs + lane] : 0x7fffffff;
     auto current_col = [&]() -> int {
         if (ptr >= be) return 0x7fffffff;
         if (ptr - chunk >= 64) {
@@ -378,20 +449,34 @@ Error from_hip(hipError_t e, const char* what) {
     return fail(kHipError, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-template <int J>
-hipError_t run_bsr(const BsrArgs& args, hipStream_t stream) {
+template <int J, int D>
+hipError_t run_wave(const BsrArgs& args, hipStream_t stream) {
     dim3 grid(ceil_div(args.block_rows, 4), ceil_div(args.N, 16 * J));
-    hipLaunchKernelGGL((bsr_mfma_kernel<J>), grid, dim3(256), 0, stream, args);
+    if (args.b_vec_ok) {
+        hipLaunchKernelGGL((bsr_wave_kernel<J, D, true>), grid, dim3(256), 0, stream, args);
+    } else {
+        hipLaunchKernelGGL((bsr_wave_kernel<J, D, false>), grid, dim3(256), 0, stream, args);
+    }
     return hipGetLastError();
+}
+
+template <int J>
+hipError_t dispatch_wave(int depth, const BsrArgs& args, hipStream_t stream) {
+    return depth == 1 ? run_wave<J, 1>(args, stream)
+                      : (depth == 2 ? run_wave<J, 2>(args, stream) : run_wave<J, 4>(args, stream));
 }
 
 template <int RG, int J>
 hipError_t run_rowgroup(const BsrArgs& args, hipStream_t stream) {
     dim3 grid(ceil_div(args.block_rows, RG), ceil_div(args.N, 16 * J));
-    // batch of 8 pairs (16 block-columns): one diagonal block of c4, a whole
-    // banded row group of c3; wide tiles take 4 to bound LDS and registers
-    constexpr int P = J >= 8 ? 4 : 8;
-    hipLaunchKernelGGL((bsr_rowgroup_kernel<RG, J, P>), grid, dim3(RG * 64), 0, stream, args);
+    // Batch of up to 8 pairs (16 block-columns: one diagonal block of c4, a
+    // whole banded row group of c3), fewer when each thread stages several
+    // 16-byte chunks per tile, to bound the staging registers (P * CPT <= 8).
+    constexpr int CPT = (32 * 2 * J + RG * 64 - 1) / (RG * 64);
+    constexpr int P = (8 / CPT) < 2 ? 2 : 8 / CPT;
+    constexpr size_t tiles_bytes = sizeof(_Float16) * P * 32 * (16 * J + 16);
+    const size_t lds = tiles_bytes + sizeof(uint32_t) * ((args.block_cols + 31) / 32);
+    hipLaunchKernelGGL((bsr_rowgroup_kernel<RG, J, P>), grid, dim3(RG * 64), lds, stream, args);
     return hipGetLastError();
 }
 
@@ -451,18 +536,27 @@ Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t strea
                  (N % 8 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0) ? 1 : 0,
                  A.block_cols};
     const BsrOpts o = opts ? *opts : BsrOpts{};
-    int j = o.tiles;
-    if (j != 1 && j != 2 && j != 4 && j != 8) j = N <= 16 ? 1 : (N <= 32 ? 2 : 4);
     hipError_t e;
     const int nwords = (A.block_cols + 31) / 32;
-    if (o.per_wave || nwords > kMaxUnionWords) {
-        // one wave per block-row, no sharing of B tiles (also the path for
-        // K beyond the union bitmap's 65536 block-columns)
-        const int jj = j > 4 ? 4 : j;
-        e = jj == 1 ? run_bsr<1>(args, stream) : (jj == 2 ? run_bsr<2>(args, stream)
-                                                          : run_bsr<4>(args, stream));
-    } else if (o.row_group == 8) {
+    const bool use_groups = o.row_group != 0 && !o.per_wave && nwords <= kMaxUnionWords;
+    if (!use_groups) {
+        // Default: the wave kernel with two 16-column tiles and two pairs in
+        // flight, measured fastest on MI355X for both the banded (c3, N = 128)
+        // and the block-diagonal (c4, N = 256) configs.
+        const int j = (o.tiles == 1 || o.tiles == 2 || o.tiles == 4) ? o.tiles : (N <= 16 ? 1 : 2);
+        const int d = (o.depth == 1 || o.depth == 2 || o.depth == 4) ? o.depth : 2;
+        e = j == 1 ? dispatch_wave<1>(d, args, stream)
+                   : (j == 2 ? dispatch_wave<2>(d, args, stream) : dispatch_wave<4>(d, args, stream));
+        return from_hip(e, "spmm_wmma launch");
+    }
+    int j = o.tiles;
+    if (j != 1 && j != 2 && j != 4 && j != 8) j = N <= 16 ? 1 : (N <= 32 ? 2 : 4);
+    if (o.row_group == 8) {
         e = dispatch_rowgroup<8>(j, args, stream);
+    } else if (o.row_group == 2) {
+        e = dispatch_rowgroup<2>(j, args, stream);
+    } else if (o.row_group == 1) {
+        e = dispatch_rowgroup<1>(j, args, stream);
     } else {
         e = dispatch_rowgroup<4>(j, args, stream);
     }

@@ -508,6 +508,7 @@ int spmm_c_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B16, float* d_C,
         o.row_group = opts->row_group;
         o.tiles     = opts->tiles;
         o.per_wave  = opts->per_wave;
+        o.depth     = opts->depth;
     }
     return from_engine(spmm::engine::launch_bsr(to_cpp(*d_bsr),
                                                 reinterpret_cast<const half*>(d_B16), d_C, N,

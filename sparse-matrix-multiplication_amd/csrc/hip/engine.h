@@ -56,11 +56,14 @@ Error launch_csr(CsrRole role, const CSR& d_A, const float* d_B, float* d_C, int
 
 Error launch_float_to_half(const float* d_src, half* d_dst, long n, hipStream_t stream);
 
-// Tuning of the BSR matrix-core kernel.  Zero fields mean "choose automatically".
+// Tuning of the BSR matrix-core kernels.  All zero selects the default: the
+// wave kernel (one independent wave per block-row) with tiles and depth
+// chosen from N.
 struct BsrOpts {
-    int row_group = 0;  // block-rows (waves) per workgroup sharing B tiles: 4 or 8
-    int tiles     = 0;  // 16-column MFMA tiles per workgroup: 1, 2, 4 or 8
-    int per_wave  = 0;  // 1: independent wave per block-row (no B sharing)
+    int row_group = 0;  // 0: wave kernel; 1, 2, 4, 8: block-rows per workgroup sharing B tiles
+    int tiles     = 0;  // 16-column MFMA tiles per wave: 1, 2, 4 (8 with row groups)
+    int per_wave  = 0;  // 1: wave kernel whatever row_group says
+    int depth     = 0;  // wave kernel: block pairs in flight per wave, 1, 2 or 4
 };
 
 Error launch_bsr(const BSR& d_A, const half* d_B, float* d_C, int N, hipStream_t stream,

@@ -71,7 +71,8 @@ class EngineOptsT(ctypes.Structure):
 
 
 class BsrOptsT(ctypes.Structure):
-    _fields_ = [("row_group", ctypes.c_int), ("tiles", ctypes.c_int), ("per_wave", ctypes.c_int)]
+    _fields_ = [("row_group", ctypes.c_int), ("tiles", ctypes.c_int), ("per_wave", ctypes.c_int),
+                ("depth", ctypes.c_int)]
 
 
 _P = ctypes.POINTER

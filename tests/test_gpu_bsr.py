@@ -91,20 +91,26 @@ def test_wmma_cases(S, O, torch, name):
     check_csr(C, C64, absC, tol=1e-5)
 
 
-@pytest.mark.parametrize("row_group,tiles,per_wave", [(4, 1, 0), (4, 2, 0), (4, 4, 0), (4, 8, 0),
+@pytest.mark.parametrize("row_group,tiles,per_wave", [(1, 1, 0), (1, 2, 0), (1, 4, 0), (1, 8, 0),
+                                                       (2, 2, 0), (2, 4, 0), (2, 8, 0),
+                                                       (4, 1, 0), (4, 2, 0), (4, 4, 0), (4, 8, 0),
                                                        (8, 1, 0), (8, 4, 0), (8, 8, 0),
                                                        (0, 1, 1), (0, 2, 1), (0, 4, 1)])
-def test_wmma_variants(S, O, torch, row_group, tiles, per_wave):
+@pytest.mark.parametrize("depth", [1, 2, 4])
+def test_wmma_variants(S, O, torch, row_group, tiles, per_wave, depth):
+    if depth != 2 and (row_group != 0 or per_wave == 0):
+        pytest.skip("depth applies to the wave kernel only")
     cases = _cases(S)
     for name in ("single_block", "odd_pair_count", "ragged_dims", "n_not_16", "n_1",
                  "empty_block_rows", "empty", "wide_n", "block_diag_small"):
         A, B = cases[name]
         hb, B16, C32, C64, absC = _refs(S, O, A, B)
-        say(f"wmma opts row_group={row_group} tiles={tiles} per_wave={per_wave} case={name}")
+        say(f"wmma opts row_group={row_group} tiles={tiles} per_wave={per_wave} depth={depth} "
+            f"case={name}")
         dA = S.DeviceBSR(hb)
         dB = torch.from_numpy(B16.view(np.int16)).cuda()
         dC = torch.full((hb.num_rows, B16.shape[1]), float("nan"), device="cuda")
-        S.spmm_wmma_opts(dA, dB, S.BsrOptsT(row_group, tiles, per_wave), dC)
+        S.spmm_wmma_opts(dA, dB, S.BsrOptsT(row_group, tiles, per_wave, depth), dC)
         torch.cuda.synchronize()
         C = dC.cpu().numpy()
         check_bsr(C, C32, absC)
@@ -119,12 +125,35 @@ def test_wmma_long_block_rows(S, O, torch):
     B = S.round_to_fp16(np.random.default_rng(3).uniform(-1, 1, (2048, 64)).astype(np.float32))
     hb, B16, C32, C64, absC = _refs(S, O, A, B)
     assert np.diff(hb.row_ptr).max() > 64
-    for rg in (4, 8):
-        say(f"wmma long block-rows row_group={rg} blocks={hb.num_blocks}")
+    for rg, tiles in ((4, 4), (8, 4), (0, 1), (0, 2), (0, 4)):
+        say(f"wmma long block-rows row_group={rg} tiles={tiles} blocks={hb.num_blocks}")
         C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
-                             S.BsrOptsT(rg, 4, 0)).cpu().numpy()
+                             S.BsrOptsT(rg, tiles, 0)).cpu().numpy()
         check_bsr(C, C32, absC)
         check_csr(C, C64, absC, tol=1e-5)
+
+
+def test_wmma_chunk_boundaries(S, O, torch):
+    # block-rows of exactly 63, 64, 65, 128 and 129 blocks: the wave kernel
+    # reads block-columns 64 at a time and multiplies them in pairs
+    rows, cols = [], []
+    for br, nb in enumerate((63, 64, 65, 128, 129, 1, 0, 2)):
+        for b in range(nb):
+            rows.append(br * 16 + (b % 16))
+            cols.append(b * 16 + (br % 16))
+    A = S.csr_from_coo_host(8 * 16, 130 * 16, np.array(rows), np.array(cols),
+                            np.random.default_rng(5).uniform(-1, 1, len(rows)).astype(np.float32))
+    A.values = S.round_to_fp16(A.values)
+    B = S.round_to_fp16(np.random.default_rng(6).uniform(-1, 1, (130 * 16, 48)).astype(np.float32))
+    hb, B16, C32, C64, absC = _refs(S, O, A, B)
+    assert list(np.diff(hb.row_ptr)) == [63, 64, 65, 128, 129, 1, 0, 2]
+    for tiles in (1, 2, 4):
+        for depth in (1, 2, 4):
+            say(f"wmma chunk boundaries tiles={tiles} depth={depth}")
+            C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
+                                 S.BsrOptsT(0, tiles, 1, depth)).cpu().numpy()
+            check_bsr(C, C32, absC)
+            check_csr(C, C64, absC, tol=1e-5)
 
 
 @pytest.mark.parametrize("cfg", ["c3", "c4"])

@@ -99,6 +99,7 @@ typedef struct spmm_bsr_opts_t {
     int tiles;     /* 16-column MFMA tiles per wave: 1, 2, 4 (8 with row groups) */
     int per_wave;  /* 1: wave kernel whatever row_group says */
     int depth;     /* wave kernel: block pairs in flight per wave: 1, 2, 4 */
+    int xcd_order; /* wave kernel: 0, 1 XCD-grouped workgroup order; 2 dispatch order */
 } spmm_bsr_opts_t;
 
 const char* spmm_c_last_error(void);

@@ -70,7 +70,28 @@ struct BsrArgs {
     int             block_rows;
     int             b_vec_ok;  // N % 8 == 0 and B 16-byte aligned
     int             block_cols;
+    int             tiles_n;    // wave kernel: column tiles (grid is 1-D)
+    int             wg_total;   // wave kernel: workgroups launched
+    int             xcd_order;  // wave kernel: 1 = XCD-grouped workgroup order
 };
+
+// Workgroup -> (block-row group, column tile) for the 1-D wave-kernel grid.
+// The hardware hands workgroup L to XCD L % 8.  With xcd_order, XCD x gets
+// the contiguous logical range [x*T/8, (x+1)*T/8) (the first T % 8 XCDs one
+// more), and logical ids run column tile fastest: each XCD works on its own
+// band of block-rows with all their column tiles, so A blocks and the B rows
+// that neighbouring block-rows share are fetched into one L2 only.
+__device__ __forceinline__ void wave_tile_of(const BsrArgs& a, int& bx, int& by) {
+    const int L = blockIdx.x;
+    int l = L;
+    if (a.xcd_order) {
+        const int xcd = L & 7, idx = L >> 3;
+        const int per = a.wg_total >> 3, rem = a.wg_total & 7;
+        l = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    }
+    bx = l / a.tiles_n;
+    by = l - bx * a.tiles_n;
+}
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
@@ -114,8 +135,10 @@ __global__ __launch_bounds__(256) void bsr_wave_kernel(BsrArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g    = lane >> 4;
     const int t    = lane & 15;
-    const int br   = blockIdx.x * 4 + wave;
-    const int n0   = blockIdx.y * NT;
+    int bx, by;
+    wave_tile_of(a, bx, by);
+    const int br   = bx * 4 + wave;
+    const int n0   = by * NT;
     if (br >= a.block_rows) return;  // waves are independent: no barrier anywhere
     _Float16* tile = s_b[wave];
 
@@ -450,8 +473,12 @@ Error from_hip(hipError_t e, const char* what) {
 }
 
 template <int J, int D>
-hipError_t run_wave(const BsrArgs& args, hipStream_t stream) {
-    dim3 grid(ceil_div(args.block_rows, 4), ceil_div(args.N, 16 * J));
+hipError_t run_wave(BsrArgs args, hipStream_t stream) {
+    args.tiles_n = ceil_div(args.N, 16 * J);
+    const long total = static_cast<long>(ceil_div(args.block_rows, 4)) * args.tiles_n;
+    if (total > 0x7fffffffL) return hipErrorInvalidConfiguration;
+    args.wg_total = static_cast<int>(total);
+    dim3 grid(args.wg_total);
     if (args.b_vec_ok) {
         hipLaunchKernelGGL((bsr_wave_kernel<J, D, true>), grid, dim3(256), 0, stream, args);
     } else {
@@ -534,8 +561,12 @@ Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t strea
                  N,
                  A.block_rows,
                  (N % 8 == 0 && reinterpret_cast<uintptr_t>(B) % 16 == 0) ? 1 : 0,
-                 A.block_cols};
+                 A.block_cols,
+                 0,
+                 0,
+                 0};
     const BsrOpts o = opts ? *opts : BsrOpts{};
+    args.xcd_order = o.xcd_order == 2 ? 0 : 1;
     hipError_t e;
     const int nwords = (A.block_cols + 31) / 32;
     const bool use_groups = o.row_group != 0 && !o.per_wave && nwords <= kMaxUnionWords;

@@ -64,6 +64,7 @@ struct BsrOpts {
     int tiles     = 0;  // 16-column MFMA tiles per wave: 1, 2, 4 (8 with row groups)
     int per_wave  = 0;  // 1: wave kernel whatever row_group says
     int depth     = 0;  // wave kernel: block pairs in flight per wave, 1, 2 or 4
+    int xcd_order = 0;  // wave kernel: 0, 1 XCD-grouped workgroup order; 2 dispatch order
 };
 
 Error launch_bsr(const BSR& d_A, const half* d_B, float* d_C, int N, hipStream_t stream,

@@ -156,6 +156,22 @@ def test_wmma_chunk_boundaries(S, O, torch):
             check_csr(C, C64, absC, tol=1e-5)
 
 
+@pytest.mark.parametrize("xcd_order", [1, 2])
+def test_wmma_workgroup_orders(S, O, torch, xcd_order):
+    # both workgroup -> tile maps of the wave kernel cover every tile once,
+    # also when the workgroup count is not a multiple of the 8 XCDs
+    cases = _cases(S)
+    for name in ("ragged_dims", "n_not_16", "empty_block_rows", "wide_n", "block_diag_small"):
+        A, B = cases[name]
+        hb, B16, C32, C64, absC = _refs(S, O, A, B)
+        for tiles in (1, 2, 4):
+            say(f"wmma xcd_order={xcd_order} tiles={tiles} case={name}")
+            C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
+                                 S.BsrOptsT(0, tiles, 1, 2, xcd_order)).cpu().numpy()
+            check_bsr(C, C32, absC)
+            check_csr(C, C64, absC, tol=1e-5)
+
+
 @pytest.mark.parametrize("cfg", ["c3", "c4"])
 def test_wmma_configs(S, O, torch, cfg):
     A, B = make_config(S, cfg)

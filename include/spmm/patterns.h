@@ -27,6 +27,10 @@ CSR generate_banded_csr(int rows, int cols, int half_bandwidth, int seed);
 CSR generate_block_diagonal_csr(int rows, int cols, int block, int seed,
                                 float value_scale = 0.1f);
 
+// The same structure with values U[-1,1) in CSR order from mt19937(seed) (the
+// value distribution of gen_matrices.py:62, used by its CLI).
+CSR generate_block_diagonal_uniform_csr(int rows, int cols, int block, int seed);
+
 // Power-law rows, as gen_matrices.py:66-81: x_r = (1 - u_r)^(-1/alpha) (Pareto
 // with x_m = 1, i.e. numpy's pareto(alpha) + 1), scaled so the sample mean is
 // mean_deg, rounded half-to-even, clipped to [1, min(cols, max_row_nnz)].

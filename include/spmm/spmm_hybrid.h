@@ -26,8 +26,14 @@ struct HybridPlan {
     const char* reason    = "";
 };
 
-// Fill-in at or below which the MFMA path wins on MI355X.
-constexpr float kHybridDefaultThreshold = 2.0f;
+// Fill-in at or below which the MFMA path wins on MI355X.  Timing both back
+// ends (spmm_tiled_v3 and spmm_wmma kernels, warm) on uniform-random inputs
+// of 4096^2 .. 16384^2 at N = 128 and 256: the MFMA path is faster at fill
+// 10 (1.3 - 2.4x) and at fill 20 (0.8 - 1.6x), the CSR engine at fill 33 and
+// above (1.0 - 1.7x); block-structured inputs cross between fill 25 and 45.
+// The reference's 2.0 was the crossover of a T4, whose tensor cores are far
+// less ahead of its CUDA cores.
+constexpr float kHybridDefaultThreshold = 24.0f;
 
 HybridPlan hybrid_choose(const CSR& h_A, int N,
                          float fill_in_threshold = kHybridDefaultThreshold);

@@ -133,6 +133,9 @@ int spmm_c_generate_banded_csr(int rows, int cols, int half_bandwidth, int seed,
                                spmm_csr_t* out);
 int spmm_c_generate_block_diagonal_csr(int rows, int cols, int block, int seed,
                                        float value_scale, spmm_csr_t* out);
+/* same structure, values U[-1,1) as gen_matrices.py:62 */
+int spmm_c_generate_block_diagonal_uniform_csr(int rows, int cols, int block, int seed,
+                                               spmm_csr_t* out);
 int spmm_c_generate_power_law_csr(int rows, int cols, double mean_deg, double alpha,
                                   int max_row_nnz, int seed, spmm_csr_t* out);
 int spmm_c_round_to_fp16(float* h_values, long n); /* values := fp32(fp16_rne(values)) */

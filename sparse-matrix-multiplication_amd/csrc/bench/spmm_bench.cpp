@@ -10,6 +10,9 @@
 //     one-event-pair-per-launch median;
 //   * hbm_gbs= / pct_hbm= price the compulsory bytes (roofline.py:177-185)
 //     against MI355X's 8 TB/s, and the MFMA path adds pct_mfma=;
+//   * cold_ms= is the median of single launches each preceded by a 512 MiB
+//     write that evicts L2 (4 MiB per XCD) and the 256 MiB MALL;
+//   * cpu_1t_ms= is one run of the same host loop on one thread;
 //   * --pattern selects the structured inputs of the BASELINE configs.
 
 #include <algorithm>
@@ -45,6 +48,8 @@ struct Args {
     int         batch = 50;
     int         cpu_threads = 0;  // 0: all hardware threads
     int         cpu_reps = 3;
+    bool        cpu_1t = true;
+    bool        cold = true;
     std::string kernel = "both";
 };
 
@@ -65,6 +70,8 @@ void print_usage(const char* prog) {
                  "                   both = baseline + memopt (default); all = every kernel\n"
                  "  --cpu-threads INT host threads of the fp64 reference (default: all)\n"
                  "  --cpu-reps INT   timed repetitions of the fp64 reference (default 3)\n"
+                 "  --no-cpu-1t      skip the one-thread run of the fp64 reference\n"
+                 "  --no-cold        skip the cold-cache (L2 and MALL flushed) timing\n"
                  "%s",
                  prog, drv::matrix_usage());
 }
@@ -95,6 +102,8 @@ Args parse_args(int argc, char** argv) {
         else if (opt == "--kernel") a.kernel = need();
         else if (opt == "--cpu-threads") a.cpu_threads = std::stoi(need());
         else if (opt == "--cpu-reps") a.cpu_reps = std::stoi(need());
+        else if (opt == "--no-cpu-1t") a.cpu_1t = false;
+        else if (opt == "--no-cold") a.cold = false;
         else if (opt == "-h" || opt == "--help") { print_usage(argv[0]); std::exit(0); }
         else if (drv::parse_matrix_opt(a.mat, opt, i, argc, argv)) {}
         else {
@@ -109,11 +118,29 @@ Args parse_args(int argc, char** argv) {
 
 struct Result {
     std::string name;
-    float time_ms = 0.f, single_ms = 0.f, gflops = 0.f;
+    float time_ms = 0.f, single_ms = 0.f, cold_ms = 0.f, gflops = 0.f;
     spmm::ErrorStats err;
     double bytes = 0.0;
     double mfma_flops = 0.0;  // executed matrix-core FLOPs (0 for CSR kernels)
 };
+
+// Scratch written before each cold launch: larger than L2 (8 x 4 MiB) plus
+// the 256 MiB MALL, so the launch finds none of its inputs on chip.
+constexpr size_t kFlushBytes = size_t(512) << 20;
+
+template <typename Launch>
+float time_cold(Launch launch, const Args& a, void* d_flush) {
+    GpuTimer t;
+    std::vector<float> cold;
+    for (int i = 0; i < a.iters; ++i) {
+        HIP_CHECK(hipMemsetAsync(d_flush, i & 0xff, kFlushBytes, nullptr));
+        t.start();
+        launch();
+        t.stop();
+        cold.push_back(t.elapsed_ms());
+    }
+    return spmm::median(cold);
+}
 
 template <typename Launch>
 void time_launches(Launch launch, const Args& a, float* batch_ms, float* single_ms) {
@@ -152,6 +179,11 @@ int main(int argc, char** argv) {
     // CPU reference (also the reported CPU baseline)
     const drv::CpuLeg cpu = drv::run_cpu_reference(h_A, h_B.data(), N, args.cpu_threads,
                                                    args.cpu_reps);
+    const double cpu_1t_ms =
+        args.cpu_1t ? drv::run_cpu_reference(h_A, h_B.data(), N, 1, 1).ms : -1.0;
+    void* d_flush = nullptr;
+    if (args.cold) HIP_CHECK(hipMalloc(&d_flush, kFlushBytes));
+    auto cold = [&](auto launch) { return args.cold ? time_cold(launch, args, d_flush) : -1.f; };
 
     spmm::CSR d_A = spmm::csr_to_device(h_A);
     float *d_B = nullptr, *d_C = nullptr;
@@ -192,6 +224,7 @@ int main(int argc, char** argv) {
         Result r;
         r.name = name;
         time_launches([&] { k.fn(d_A, d_B, d_C, N); }, args, &r.time_ms, &r.single_ms);
+        r.cold_ms = cold([&] { k.fn(d_A, d_B, d_C, N); });
         fetch_compare(r);
         finish(r);
         r.bytes = drv::csr_bytes(M, K, N, h_A.nnz);
@@ -214,6 +247,7 @@ int main(int argc, char** argv) {
         r.name = "wmma";
         time_launches([&] { spmm::spmm_wmma(d_bsr, d_B16, d_C, N); }, args, &r.time_ms,
                       &r.single_ms);
+        r.cold_ms = cold([&] { spmm::spmm_wmma(d_bsr, d_B16, d_C, N); });
         fetch_compare(r);
         finish(r);
         r.bytes = drv::bsr_bytes(M, K, N, h_bsr.num_blocks);
@@ -235,6 +269,7 @@ int main(int argc, char** argv) {
         r.time_ms = spmm::spmm_hybrid_run(plan, h_A, h_B.data(), h_C.data(), N, args.warmup,
                                           args.iters);
         r.single_ms = r.time_ms;
+        r.cold_ms = -1.f;  // host-in/host-out call: not timed cold
         r.err = spmm::compare(h_C, cpu.C);
         finish(r);
         r.bytes = drv::csr_bytes(M, K, N, h_A.nnz);
@@ -254,14 +289,18 @@ int main(int argc, char** argv) {
                     r.name.c_str(), M, K, N, h_A.nnz, density, r.time_ms, r.gflops,
                     r.err.max_abs, r.err.max_rel, r.err.rel_l2, r.single_ms, gbs,
                     100.0 * gbs / drv::kHbmPeakGBs);
+        if (r.cold_ms > 0) std::printf(" cold_ms=%.4f", r.cold_ms);
         if (r.mfma_flops > 0) {
             const double mf = r.mfma_flops / (static_cast<double>(r.time_ms) * 1.0e6);
             std::printf(" pct_mfma=%.2f", 100.0 * mf / drv::kMfmaF16Peak);
         }
-        std::printf(" cpu_ms=%.3f cpu_threads=%d cpu_gflops=%.2f\n", cpu.ms, cpu.threads,
+        std::printf(" cpu_ms=%.3f cpu_threads=%d cpu_gflops=%.2f", cpu.ms, cpu.threads,
                     flops / (cpu.ms * 1.0e6));
+        if (cpu_1t_ms > 0) std::printf(" cpu_1t_ms=%.3f", cpu_1t_ms);
+        std::printf("\n");
     }
 
+    if (d_flush != nullptr) HIP_CHECK(hipFree(d_flush));
     HIP_CHECK(hipFree(d_B));
     HIP_CHECK(hipFree(d_C));
     spmm::csr_free_device(d_A);

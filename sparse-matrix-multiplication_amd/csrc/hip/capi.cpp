@@ -392,6 +392,15 @@ int spmm_c_generate_block_diagonal_csr(int rows, int cols, int block, int seed, 
     });
 }
 
+int spmm_c_generate_block_diagonal_uniform_csr(int rows, int cols, int block, int seed,
+                                               spmm_csr_t* out) {
+    if (out == nullptr) return set_error(SPMM_INVALID, "null output");
+    return guarded([&] {
+        *out = to_c(spmm::generate_block_diagonal_uniform_csr(rows, cols, block, seed));
+        return ok();
+    });
+}
+
 int spmm_c_generate_power_law_csr(int rows, int cols, double mean_deg, double alpha, int cap,
                                   int seed, spmm_csr_t* out) {
     if (out == nullptr) return set_error(SPMM_INVALID, "null output");

@@ -86,6 +86,28 @@ CSR generate_block_diagonal_csr(int rows, int cols, int block, int seed, float v
     return csr_from_rows(rows, cols, rp, ci, va);
 }
 
+CSR generate_block_diagonal_uniform_csr(int rows, int cols, int block, int seed) {
+    check_dims(rows, cols, "generate_block_diagonal_uniform_csr");
+    if (block < 1) throw std::runtime_error("generate_block_diagonal_uniform_csr: block must be >= 1");
+    std::mt19937 rng(static_cast<uint32_t>(seed));
+    std::uniform_real_distribution<float> uni(-1.f, 1.f);
+    const int nblk = std::min(rows, cols) / block;
+    std::vector<int> rp(static_cast<size_t>(rows) + 1, 0);
+    std::vector<int> ci;
+    std::vector<float> va;
+    for (int r = 0; r < rows; ++r) {
+        const int b = r / block;
+        if (b < nblk) {
+            for (int c = b * block; c < (b + 1) * block; ++c) {
+                ci.push_back(c);
+                va.push_back(uni(rng));
+            }
+        }
+        rp[static_cast<size_t>(r) + 1] = static_cast<int>(ci.size());
+    }
+    return csr_from_rows(rows, cols, rp, ci, va);
+}
+
 CSR generate_power_law_csr(int rows, int cols, double mean_deg, double alpha,
                            int max_row_nnz, int seed) {
     check_dims(rows, cols, "generate_power_law_csr");

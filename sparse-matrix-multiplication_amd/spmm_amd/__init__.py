@@ -100,6 +100,7 @@ _SIGNATURES = {
     "spmm_c_generate_dense_row_major": (_int, [_int, _int, _int, _vp]),
     "spmm_c_generate_banded_csr": (_int, [_int, _int, _int, _int, _P(CsrT)]),
     "spmm_c_generate_block_diagonal_csr": (_int, [_int, _int, _int, _int, _float, _P(CsrT)]),
+    "spmm_c_generate_block_diagonal_uniform_csr": (_int, [_int, _int, _int, _int, _P(CsrT)]),
     "spmm_c_generate_power_law_csr": (_int, [_int, _int, _double, _double, _int, _int, _P(CsrT)]),
     "spmm_c_round_to_fp16": (_int, [_vp, _long]),
     "spmm_c_nnz_balanced_bounds": (_int, [_P(CsrT), _int, _vp]),
@@ -281,6 +282,14 @@ def generate_block_diagonal_csr(rows: int, cols: int, block: int, seed: int,
     s = CsrT()
     _check(lib().spmm_c_generate_block_diagonal_csr(rows, cols, block, seed, value_scale,
                                                     ctypes.byref(s)))
+    return _csr_from_struct(s)
+
+
+def generate_block_diagonal_uniform_csr(rows: int, cols: int, block: int, seed: int) -> HostCSR:
+    """Block-diagonal structure with U[-1,1) values (gen_matrices.py:51-63)."""
+    s = CsrT()
+    _check(lib().spmm_c_generate_block_diagonal_uniform_csr(rows, cols, block, seed,
+                                                            ctypes.byref(s)))
     return _csr_from_struct(s)
 
 

@@ -34,6 +34,38 @@ def test_hybrid_plan_and_run(S, O, cfg):
         check_bsr(C, C32, absC)
 
 
+def _kernel_us(S, torch, kernel, dA, dB, dC, reps=50):
+    S.launch_repeat(kernel, dA, dB, dC, 5)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    best = float("inf")
+    for _ in range(3):
+        e0.record()
+        S.launch_repeat(kernel, dA, dB, dC, reps)
+        e1.record()
+        torch.cuda.synchronize()
+        best = min(best, e0.elapsed_time(e1) / reps * 1000.0)
+    return best
+
+
+@pytest.mark.parametrize("cfg", sorted(CONFIGS))
+def test_hybrid_picks_faster_backend(S, cfg):
+    # the default plan names the back end whose kernel is faster on this GPU
+    import torch
+    A, B = make_config(S, cfg)
+    N = B.shape[1]
+    plan = S.hybrid_choose(A, N)
+    dB = torch.from_numpy(B).cuda()
+    dC = torch.empty((A.num_rows, N), device="cuda")
+    t_csr = _kernel_us(S, torch, "tiled_v3", S.DeviceCSR(A), dB, dC)
+    t_mma = _kernel_us(S, torch, "wmma", S.DeviceBSR(S.bsr_from_csr_host(A)),
+                       S.float_to_half(dB), dC)
+    print(f"hybrid config={cfg} csr_us={t_csr:.2f} wmma_us={t_mma:.2f} "
+          f"plan={plan.backend_name}", flush=True)
+    assert plan.backend_name == ("wmma" if t_mma < t_csr else "csr")
+
+
 def test_hybrid_forced_backends_agree(S, O):
     # both back ends on the same fp16-exact input give the same product
     A, B = make_config(S, "c3")

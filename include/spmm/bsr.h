@@ -69,4 +69,20 @@ void bsr_free_device(BSR& d);
 // bsr.cu:149-162.
 BSR_stats bsr_compute_stats(const BSR_host& h);
 
+// Additions (no counterpart in the reference, whose BSR build is host-only):
+
+// bsr_compute_stats(bsr_from_csr_host(h_csr)) from one counting pass over the
+// CSR, without building the fp16 blocks.
+BSR_stats bsr_stats_from_csr_host(const CSR& h_csr);
+
+// CSR -> BSR on the device from a device CSR: the same row_ptr, col_idx and
+// fp16 values as bsr_from_csr_host, built next to the kernels (allocates the
+// three arrays; release with bsr_free_device).  Column indices must ascend
+// within each row (repeats allowed, adjacent; the last is kept) and
+// num_cols <= 4128768.  Errors print and exit, like the reference's wrappers.
+BSR bsr_from_csr_device(const CSR& d_csr);
+
+// Fill-in statistics of a device CSR, same contract as bsr_from_csr_device.
+BSR_stats bsr_stats_from_csr_device(const CSR& d_csr);
+
 }  // namespace spmm

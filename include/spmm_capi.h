@@ -126,6 +126,17 @@ void spmm_c_bsr_free_host(spmm_bsr_t* h);                                  /* BS
 int spmm_c_bsr_to_device(const spmm_bsr_t* h, spmm_bsr_t* d_out);          /* bsr.h:74 */
 int spmm_c_bsr_free_device(spmm_bsr_t* d);                                 /* bsr.h:77 */
 int spmm_c_bsr_compute_stats(const spmm_bsr_t* h, spmm_bsr_stats_t* out);  /* bsr.h:80 */
+/* Additions with no reference counterpart (the reference builds BSR on the host
+ * only, bsr.cu:30-109): stats of a host CSR without building the blocks; CSR ->
+ * BSR and its stats on the device from a device CSR (column indices ascending
+ * within each row, num_cols <= 4128768; SPMM_UNSUPPORTED otherwise; the device
+ * BSR is released with spmm_c_bsr_free_device); device BSR -> host copy
+ * (release with spmm_c_bsr_free_host). */
+int spmm_c_bsr_stats_from_csr_host(const spmm_csr_t* h, spmm_bsr_stats_t* out);
+int spmm_c_bsr_from_csr_device(const spmm_csr_t* d_A, spmm_bsr_t* d_out, void* stream);
+int spmm_c_bsr_stats_from_csr_device(const spmm_csr_t* d_A, spmm_bsr_stats_t* out,
+                                     void* stream);
+int spmm_c_bsr_to_host(const spmm_bsr_t* d, spmm_bsr_t* h_out);
 
 /* ---- synthetic inputs (harness.cu:114-120, gen_matrices.py:37-81) ----- */
 int spmm_c_generate_dense_row_major(int rows, int cols, int seed, float* h_out);

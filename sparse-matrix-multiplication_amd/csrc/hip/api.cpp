@@ -62,6 +62,18 @@ void float_to_half(const float* d_src, half* d_dst, int n_elements) {
                   "float_to_half");
 }
 
+BSR bsr_from_csr_device(const CSR& d_csr) {
+    BSR out;
+    exit_on_error(engine::build_bsr_device(d_csr, &out, nullptr), "bsr_from_csr_device");
+    return out;
+}
+
+BSR_stats bsr_stats_from_csr_device(const CSR& d_csr) {
+    BSR_stats out{};
+    exit_on_error(engine::bsr_stats_device(d_csr, &out, nullptr), "bsr_stats_from_csr_device");
+    return out;
+}
+
 void spmm_wmma(const BSR& d_bsr, const half* d_B_fp16, float* d_C, int N) {
     exit_on_error(engine::launch_bsr(d_bsr, d_B_fp16, d_C, N, nullptr), "spmm_wmma");
 }

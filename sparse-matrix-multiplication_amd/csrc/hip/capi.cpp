@@ -2,6 +2,7 @@
 
 #include "spmm_capi.h"
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <new>
@@ -359,6 +360,86 @@ int spmm_c_bsr_compute_stats(const spmm_bsr_t* h, spmm_bsr_stats_t* out) {
     out->original_nnz    = s.original_nnz;
     out->fill_in_ratio   = s.fill_in_ratio;
     out->block_density   = s.block_density;
+    return ok();
+}
+
+namespace {
+
+void stats_to_c(const spmm::BSR_stats& s, spmm_bsr_stats_t* out) {
+    out->num_blocks      = s.num_blocks;
+    out->stored_elements = s.stored_elements;
+    out->original_nnz    = s.original_nnz;
+    out->fill_in_ratio   = s.fill_in_ratio;
+    out->block_density   = s.block_density;
+}
+
+}  // namespace
+
+int spmm_c_bsr_stats_from_csr_host(const spmm_csr_t* h, spmm_bsr_stats_t* out) {
+    if (h == nullptr || out == nullptr) return set_error(SPMM_INVALID, "null argument");
+    return guarded([&] {
+        stats_to_c(spmm::bsr_stats_from_csr_host(to_cpp(*h)), out);
+        return ok();
+    });
+}
+
+int spmm_c_bsr_from_csr_device(const spmm_csr_t* d_A, spmm_bsr_t* d_out, void* stream) {
+    if (d_A == nullptr || d_out == nullptr) return set_error(SPMM_INVALID, "null argument");
+    spmm::BSR b;
+    const int rc = from_engine(spmm::engine::build_bsr_device(to_cpp(*d_A), &b, as_stream(stream)));
+    if (rc != SPMM_OK) return rc;
+    spmm_bsr_t r;
+    r.num_rows   = b.num_rows;
+    r.num_cols   = b.num_cols;
+    r.block_rows = b.block_rows;
+    r.block_cols = b.block_cols;
+    r.num_blocks = b.num_blocks;
+    r.nnz        = b.nnz;
+    r.row_ptr    = b.row_ptr;
+    r.col_idx    = b.col_idx;
+    r.values     = reinterpret_cast<uint16_t*>(b.values);
+    *d_out = r;
+    return ok();
+}
+
+int spmm_c_bsr_stats_from_csr_device(const spmm_csr_t* d_A, spmm_bsr_stats_t* out, void* stream) {
+    if (d_A == nullptr || out == nullptr) return set_error(SPMM_INVALID, "null argument");
+    spmm::BSR_stats s{};
+    const int rc = from_engine(spmm::engine::bsr_stats_device(to_cpp(*d_A), &s, as_stream(stream)));
+    if (rc != SPMM_OK) return rc;
+    stats_to_c(s, out);
+    return ok();
+}
+
+int spmm_c_bsr_to_host(const spmm_bsr_t* d, spmm_bsr_t* h_out) {
+    if (d == nullptr || h_out == nullptr || d->block_rows < 0 || d->num_blocks < 0) {
+        return set_error(SPMM_INVALID, "spmm_c_bsr_to_host: bad argument");
+    }
+    spmm_bsr_t r = *d;
+    const size_t rp = static_cast<size_t>(d->block_rows) + 1;
+    const size_t nb = static_cast<size_t>(d->num_blocks);
+    r.row_ptr = static_cast<int*>(std::malloc(sizeof(int) * rp));
+    r.col_idx = static_cast<int*>(std::malloc(sizeof(int) * std::max<size_t>(nb, 1)));
+    r.values  = static_cast<uint16_t*>(std::malloc(sizeof(uint16_t) * std::max<size_t>(nb * 256, 1)));
+    if (r.row_ptr == nullptr || r.col_idx == nullptr || r.values == nullptr) {
+        spmm_c_bsr_free_host(&r);
+        return set_error(SPMM_NO_MEMORY, "spmm_c_bsr_to_host: out of host memory");
+    }
+    int rc = from_hip(hipMemcpy(r.row_ptr, d->row_ptr, sizeof(int) * rp, hipMemcpyDeviceToHost),
+                      "hipMemcpy");
+    if (rc == SPMM_OK && nb > 0) {
+        rc = from_hip(hipMemcpy(r.col_idx, d->col_idx, sizeof(int) * nb, hipMemcpyDeviceToHost),
+                      "hipMemcpy");
+        if (rc == SPMM_OK) {
+            rc = from_hip(hipMemcpy(r.values, d->values, sizeof(uint16_t) * nb * 256,
+                                    hipMemcpyDeviceToHost), "hipMemcpy");
+        }
+    }
+    if (rc != SPMM_OK) {
+        spmm_c_bsr_free_host(&r);
+        return rc;
+    }
+    *h_out = r;
     return ok();
 }
 

@@ -503,8 +503,16 @@ Error launch_csr(CsrRole role, const CSR& A, const float* B, float* C, int N,
         return fail(kInvalid, "engine vec must be 1, 2 or 4");
     }
     const int vec = pick_vec(N, B, C, want_vec);
-    // Column slices (XCD-aware, see the kernel): 1, 2, 4 or 8.
+    // Column slices (XCD-aware, see the kernel): 1, 2, 4 or 8.  Automatic:
+    // one slice per 128 columns once B rows are wider than that, so each XCD
+    // gathers 512-byte row pieces of a B slice that fits its L2 (measured on
+    // MI355X: N = 256 -> 2 slices, 1.15-1.45x; N = 512 -> 4 slices, 1.5-1.7x;
+    // N = 128 -> 1, where slicing only shortens the gathers).
     int slices = o.slices;
+    if (slices == 0 && vec == 4 && role != CsrRole::Tiled) {
+        slices = 1;
+        while (slices < 8 && N >= 256 * slices) slices *= 2;
+    }
     if (slices != 1 && slices != 2 && slices != 4 && slices != 8) slices = 1;
     int slice_cols = ceil_div(N, slices);
     slice_cols = ceil_div(slice_cols, vec) * vec;

@@ -70,6 +70,15 @@ struct BsrOpts {
 Error launch_bsr(const BSR& d_A, const half* d_B, float* d_C, int N, hipStream_t stream,
                  const BsrOpts* opts = nullptr);
 
+// CSR -> BSR on the device: allocates the BSR's three arrays (release with
+// bsr_free_device) and fills them exactly as bsr_from_csr_host would.  The
+// CSR's column indices must ascend within each row (repeats adjacent).
+Error build_bsr_device(const CSR& d_A, BSR* out, hipStream_t stream);
+
+// Fill-in statistics of a device CSR (the numbers bsr_compute_stats gives
+// for bsr_from_csr_host of the same matrix), without building the values.
+Error bsr_stats_device(const CSR& d_A, BSR_stats* out, hipStream_t stream);
+
 // Number of workgroups the engine uses for an explicit partition of this CSR.
 int default_partition_parts(int num_rows, int nnz);
 

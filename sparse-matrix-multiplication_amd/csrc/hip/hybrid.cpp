@@ -44,7 +44,9 @@ HybridPlan hybrid_choose(const CSR& h_A, int N, float fill_in_threshold) {
     HybridPlan plan;
     plan.threshold = fill_in_threshold;
     plan.n_aligned = N > 0 && N % BSR_BLOCK == 0;
-    const BSR_stats st = bsr_compute_stats(bsr_from_csr_host(h_A));
+    // The reference builds the whole BSR here only to read its statistics
+    // (spmm_hybrid.cu:38); counting blocks gives the same numbers.
+    const BSR_stats st = bsr_stats_from_csr_host(h_A);
     plan.fill_in_ratio = st.fill_in_ratio;
     plan.block_density = st.block_density;
     if (plan.n_aligned && st.fill_in_ratio <= fill_in_threshold) {
@@ -78,8 +80,21 @@ float spmm_hybrid_run(const HybridPlan& plan, const CSR& h_A, const float* h_B, 
 
     float ms = 0.f;
     if (plan.backend == Backend::TENSOR_WMMA) {
-        const BSR_host h_bsr = bsr_from_csr_host(h_A);
-        BSR d_bsr = bsr_to_device(h_bsr);
+        // Upload the CSR (8 bytes per nonzero; the BSR is 512 bytes per block)
+        // and build the BSR on the device.  Inputs the device builder does not
+        // take (rows with descending column indices, num_cols > 4128768) are
+        // built on the host as in the reference (spmm_hybrid.cu:78-80).
+        BSR d_bsr;
+        {
+            CSR d_A = csr_to_device(h_A);
+            const engine::Error built = engine::build_bsr_device(d_A, &d_bsr, nullptr);
+            csr_free_device(d_A);
+            if (built.status == engine::kUnsupported) {
+                d_bsr = bsr_to_device(bsr_from_csr_host(h_A));
+            } else {
+                exit_on_error(built, "spmm_hybrid_run");
+            }
+        }
         half* d_B16 = nullptr;
         HIP_CHECK(hipMalloc(&d_B16, sizeof(half) * (b_elems > 0 ? b_elems : 1)));
         exit_on_error(engine::launch_float_to_half(d_B, d_B16, static_cast<long>(b_elems), nullptr),

@@ -96,6 +96,35 @@ void bsr_free_device(BSR& d) {
     if (d.values)  { HIP_CHECK(hipFree(d.values));  d.values  = nullptr; }
 }
 
+BSR_stats bsr_stats_from_csr_host(const CSR& h) {
+    constexpr int BS = BSR_BLOCK;
+    const int block_rows = (h.num_rows + BS - 1) / BS;
+    const int block_cols = (h.num_cols + BS - 1) / BS;
+    std::vector<int> stamp(static_cast<size_t>(block_cols), 0);
+    long blocks = 0;
+    for (int br = 0; br < block_rows; ++br) {
+        const int r_end = std::min(h.num_rows, (br + 1) * BS);
+        for (int p = h.row_ptr[br * BS]; p < h.row_ptr[r_end]; ++p) {
+            const int c = h.col_idx[p];
+            if (c < 0 || c >= h.num_cols) {
+                throw std::runtime_error("bsr_stats_from_csr_host: column index out of range");
+            }
+            if (stamp[c / BS] != br + 1) {
+                stamp[c / BS] = br + 1;
+                ++blocks;
+            }
+        }
+    }
+    BSR_host shape;  // the statistics read only the scalar fields
+    shape.num_rows   = h.num_rows;
+    shape.num_cols   = h.num_cols;
+    shape.block_rows = block_rows;
+    shape.block_cols = block_cols;
+    shape.num_blocks = static_cast<int>(blocks);
+    shape.nnz        = h.nnz;
+    return bsr_compute_stats(shape);
+}
+
 BSR_stats bsr_compute_stats(const BSR_host& h) {
     BSR_stats s;
     s.num_blocks      = h.num_blocks;

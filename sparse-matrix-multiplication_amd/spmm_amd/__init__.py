@@ -101,6 +101,10 @@ _SIGNATURES = {
     "spmm_c_generate_banded_csr": (_int, [_int, _int, _int, _int, _P(CsrT)]),
     "spmm_c_generate_block_diagonal_csr": (_int, [_int, _int, _int, _int, _float, _P(CsrT)]),
     "spmm_c_generate_block_diagonal_uniform_csr": (_int, [_int, _int, _int, _int, _P(CsrT)]),
+    "spmm_c_bsr_stats_from_csr_host": (_int, [_P(CsrT), _P(BsrStatsT)]),
+    "spmm_c_bsr_from_csr_device": (_int, [_P(CsrT), _P(BsrT), _vp]),
+    "spmm_c_bsr_stats_from_csr_device": (_int, [_P(CsrT), _P(BsrStatsT), _vp]),
+    "spmm_c_bsr_to_host": (_int, [_P(BsrT), _P(BsrT)]),
     "spmm_c_generate_power_law_csr": (_int, [_int, _int, _double, _double, _int, _int, _P(CsrT)]),
     "spmm_c_round_to_fp16": (_int, [_vp, _long]),
     "spmm_c_nnz_balanced_bounds": (_int, [_P(CsrT), _int, _vp]),
@@ -361,6 +365,14 @@ def bsr_compute_stats(b: HostBSR) -> BsrStatsT:
     return st
 
 
+def bsr_stats_from_csr_host(m: HostCSR) -> BsrStatsT:
+    """bsr_compute_stats(bsr_from_csr_host(m)) without building the blocks."""
+    st = BsrStatsT()
+    src = m.struct()
+    _check(lib().spmm_c_bsr_stats_from_csr_host(ctypes.byref(src), ctypes.byref(st)))
+    return st
+
+
 def nnz_balanced_bounds(m: HostCSR, parts: int) -> np.ndarray:
     out = np.empty(parts + 1, dtype=np.int32)
     src = m.struct()
@@ -486,6 +498,53 @@ class DeviceBSR:
                     self.num_blocks, self.nnz, self.row_ptr.data_ptr(),
                     self.col_idx.data_ptr() if self.num_blocks else 0,
                     self.values.data_ptr() if self.num_blocks else 0)
+
+
+class BuiltDeviceBSR:
+    """A device BSR whose arrays the library allocated (bsr_from_csr_device);
+    released with spmm_c_bsr_free_device when the object goes away."""
+
+    def __init__(self, s: BsrT):
+        self._s = s
+        self.num_rows, self.num_cols = s.num_rows, s.num_cols
+        self.block_rows, self.block_cols = s.block_rows, s.block_cols
+        self.num_blocks, self.nnz = s.num_blocks, s.nnz
+
+    def struct(self) -> BsrT:
+        return self._s
+
+    def to_host(self) -> HostBSR:
+        h = BsrT()
+        _check(lib().spmm_c_bsr_to_host(ctypes.byref(self._s), ctypes.byref(h)))
+        return _bsr_from_struct(h)
+
+    def free(self) -> None:
+        if self._s is not None:
+            lib().spmm_c_bsr_free_device(ctypes.byref(self._s))
+            self._s = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:  # interpreter shutdown
+            pass
+
+
+def bsr_from_csr_device(A: DeviceCSR, stream=None) -> BuiltDeviceBSR:
+    """CSR -> BSR on the device (same arrays as bsr_from_csr_host)."""
+    s = BsrT()
+    src = A.struct()
+    _check(lib().spmm_c_bsr_from_csr_device(ctypes.byref(src), ctypes.byref(s),
+                                            _stream_handle(stream)))
+    return BuiltDeviceBSR(s)
+
+
+def bsr_stats_from_csr_device(A: DeviceCSR, stream=None) -> BsrStatsT:
+    st = BsrStatsT()
+    src = A.struct()
+    _check(lib().spmm_c_bsr_stats_from_csr_device(ctypes.byref(src), ctypes.byref(st),
+                                                  _stream_handle(stream)))
+    return st
 
 
 def spmm_csr(kernel: str, A: DeviceCSR, B, C=None, stream=None):

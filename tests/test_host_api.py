@@ -218,3 +218,18 @@ def test_host_reference_equals_oracle(S, O):
     for threads in (1, 3):
         C = S.host_reference_f64(A, B, threads)
         assert np.array_equal(C, C64.astype(np.float32))
+
+
+def test_bsr_stats_from_csr_host_equals_full_build(S):
+    cases = [S.generate_uniform_random_csr(300, 500, 0.03, 1),
+             S.generate_banded_csr(1000, 1000, 37, 3),
+             S.generate_power_law_csr(3000, 2500, 40.0, 1.5, 2500, 5),
+             S.csr_from_coo_host(48, 128, [0, 0, 5, 17, 17], [3, 3, 9, 100, 2],
+                                 [1.0, 2.0, 3.0, 4.0, 5.0]),
+             S.csr_from_coo_host(77, 33, [], [], [])]
+    for A in cases:
+        fast = S.bsr_stats_from_csr_host(A)
+        full = S.bsr_compute_stats(S.bsr_from_csr_host(A))
+        for f in ("num_blocks", "stored_elements", "original_nnz", "fill_in_ratio",
+                  "block_density"):
+            assert getattr(fast, f) == getattr(full, f), f

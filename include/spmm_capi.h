@@ -199,6 +199,13 @@ float spmm_c_hybrid_default_threshold(void);
 int spmm_c_hybrid_choose(const spmm_csr_t* h_A, int N, float fill_in_threshold,
                          spmm_hybrid_plan_t* out);               /* spmm_hybrid.h:48 */
 const char* spmm_c_backend_name(int backend);                    /* spmm_hybrid.h:51 */
+/* ---- unified memory on one GPU (spmm_multigpu.h:32, :54-58) ----------- */
+int spmm_c_gpu_count(void);                                                /* spmm_multigpu.h:32 */
+/* A, B, C in managed memory, prefetched, tiled_v3 engine; *prefetched_out is 0
+ * when the device could not prefetch (pages then move on first touch). */
+int spmm_c_unified(const spmm_csr_t* h_A, const float* h_B, float* h_C, int N, int warmup,
+                   int iters, float* ms_out, int* prefetched_out);     /* spmm_multigpu.h:57 */
+
 int spmm_c_hybrid_run(const spmm_hybrid_plan_t* plan, const spmm_csr_t* h_A,
                       const float* h_B, float* h_C, int N, int warmup, int iters,
                       float* ms_out);                            /* spmm_hybrid.h:62 */

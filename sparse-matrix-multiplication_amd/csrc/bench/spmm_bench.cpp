@@ -36,6 +36,7 @@
 #include "spmm/metrics.h"
 #include "spmm/patterns.h"
 #include "spmm/spmm_hybrid.h"
+#include "spmm/spmm_multigpu.h"
 #include "spmm/utils.h"
 
 namespace {
@@ -66,7 +67,7 @@ void print_usage(const char* prog) {
                  "  --batch INT      launches per timed batch (default 50)\n"
                  "  --bin PATH       load CSR from binary file (overrides --m/--k/--density)\n"
                  "  --kernel STR     baseline | memopt | memopt_v2 | tiled | tiled_v2 | tiled_v3\n"
-                 "                   | tiled_v4 | wmma | hybrid | both | all\n"
+                 "                   | tiled_v4 | wmma | hybrid | unified | both | all\n"
                  "                   both = baseline + memopt (default); all = every kernel\n"
                  "  --cpu-threads INT host threads of the fp64 reference (default: all)\n"
                  "  --cpu-reps INT   timed repetitions of the fp64 reference (default 3)\n"
@@ -276,9 +277,22 @@ int main(int argc, char** argv) {
         results.push_back(r);
     }
 
-    if (ks == "multigpu" || ks == "unified") {
-        std::fprintf(stderr, "kernel '%s' is not part of this single-GPU engine. Skipping.\n",
-                     ks.c_str());
+    if (ks == "unified") {
+        std::vector<float> h_C(static_cast<size_t>(M) * N);
+        Result r;
+        r.name = "unified";
+        r.time_ms = spmm::spmm_unified(h_A, h_B.data(), h_C.data(), N, args.warmup, args.iters);
+        r.single_ms = r.time_ms;
+        r.cold_ms = -1.f;  // host-in/host-out call: not timed cold
+        r.err = spmm::compare(h_C, cpu.C);
+        finish(r);
+        r.bytes = drv::csr_bytes(M, K, N, h_A.nnz);
+        results.push_back(r);
+    }
+
+    if (ks == "multigpu") {
+        std::fprintf(stderr, "kernel 'multigpu' is not part of this single-GPU engine. "
+                             "Skipping.\n");
     }
 
     for (const Result& r : results) {

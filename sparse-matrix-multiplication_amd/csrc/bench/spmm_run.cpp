@@ -4,9 +4,9 @@
 // verify, print the plan= and run= lines.
 //
 // Differences: verification uses the host fp64 loop instead of cuSPARSE (the
-// [PASS] rule, rel_l2 < 1e-2, is unchanged); --multi-gpu and --unified are not
-// part of this single-GPU engine and are rejected; --pattern selects the
-// structured inputs of the BASELINE configs.
+// [PASS] rule, rel_l2 < 1e-2, is unchanged); --multi-gpu is not part of this
+// single-GPU engine and is rejected; --pattern selects the structured inputs
+// of the BASELINE configs.
 
 #include <cstdio>
 #include <cstdlib>
@@ -18,6 +18,7 @@
 #include "spmm/metrics.h"
 #include "spmm/patterns.h"
 #include "spmm/spmm_hybrid.h"
+#include "spmm/spmm_multigpu.h"
 
 namespace {
 
@@ -28,6 +29,7 @@ struct Args {
     int   iters = 10;
     float threshold = spmm::kHybridDefaultThreshold;
     bool  verify = true;
+    bool  unified = false;
     int   cpu_threads = 0;
 };
 
@@ -44,6 +46,7 @@ void print_usage(const char* prog) {
                  "  --threshold FLT  BSR fill-in cut-off for the MFMA path (default %.2f)\n"
                  "  --bin PATH       load CSR from a binary file (overrides --m/--k/--density)\n"
                  "  --no-verify      skip the host fp64 correctness check\n"
+                 "  --unified        single-GPU unified-memory path (CSR engine)\n"
                  "  --cpu-threads INT host threads of the verification loop (default: all)\n"
                  "%s",
                  prog, static_cast<double>(spmm::kHybridDefaultThreshold), drv::matrix_usage());
@@ -74,7 +77,8 @@ Args parse_args(int argc, char** argv) {
         else if (opt == "--bin") a.mat.bin_path = need();
         else if (opt == "--no-verify") a.verify = false;
         else if (opt == "--cpu-threads") a.cpu_threads = std::stoi(need());
-        else if (opt == "--multi-gpu" || opt == "--unified" || opt == "--gpus") {
+        else if (opt == "--unified") a.unified = true;
+        else if (opt == "--multi-gpu" || opt == "--gpus") {
             std::fprintf(stderr, "%s is not part of this single-GPU engine\n", opt.c_str());
             std::exit(EXIT_FAILURE);
         } else if (opt == "-h" || opt == "--help") {
@@ -104,9 +108,16 @@ int main(int argc, char** argv) {
     std::vector<float> h_C(static_cast<size_t>(M) * N, 0.f);
 
     const spmm::HybridPlan plan = spmm::hybrid_choose(h_A, N, args.threshold);
-    const float ms = spmm::spmm_hybrid_run(plan, h_A, h_B.data(), h_C.data(), N, args.warmup,
-                                           args.iters);
-    const std::string mode = std::string("hybrid[") + spmm::backend_name(plan.backend) + "]";
+    float ms = 0.f;
+    std::string mode;
+    if (args.unified) {
+        ms   = spmm::spmm_unified(h_A, h_B.data(), h_C.data(), N, args.warmup, args.iters);
+        mode = "unified[csr]";
+    } else {
+        ms   = spmm::spmm_hybrid_run(plan, h_A, h_B.data(), h_C.data(), N, args.warmup,
+                                     args.iters);
+        mode = std::string("hybrid[") + spmm::backend_name(plan.backend) + "]";
+    }
     const double flops = 2.0 * static_cast<double>(h_A.nnz) * N;
     const double gflops = flops / (static_cast<double>(ms) * 1.0e6);
 

@@ -654,9 +654,37 @@ int spmm_c_hybrid_run(const spmm_hybrid_plan_t* plan, const spmm_csr_t* h_A, con
         p.threshold     = plan->threshold;
         p.n_aligned     = plan->n_aligned != 0;
         p.reason        = plan->reason ? plan->reason : "";
-        const float ms  = spmm::spmm_hybrid_run(p, to_cpp(*h_A), h_B, h_C, N, warmup, iters);
-        if (ms_out) *ms_out = ms;
-        return ok();
+        float ms = 0.f;
+        const int rc = from_engine(
+            spmm::engine::run_hybrid(p, to_cpp(*h_A), h_B, h_C, N, warmup, iters, &ms));
+        if (rc == SPMM_OK && ms_out) *ms_out = ms;
+        return rc;
+    });
+}
+
+int spmm_c_gpu_count(void) {
+    int n = 0;
+    return hipGetDeviceCount(&n) == hipSuccess ? n : 0;
+}
+
+int spmm_c_unified(const spmm_csr_t* h_A, const float* h_B, float* h_C, int N, int warmup,
+                   int iters, float* ms_out, int* prefetched_out) {
+    if (h_A == nullptr || h_C == nullptr || N < 0 || warmup < 0 || iters < 0) {
+        return set_error(SPMM_INVALID, "bad argument");
+    }
+    if (h_B == nullptr && static_cast<long>(h_A->num_cols) * N > 0) {
+        return set_error(SPMM_INVALID, "null B");
+    }
+    return guarded([&] {
+        float ms = 0.f;
+        bool moved = true;
+        const int rc = from_engine(spmm::engine::run_unified(to_cpp(*h_A), h_B, h_C, N, warmup,
+                                                             iters, &ms, &moved));
+        if (rc == SPMM_OK) {
+            if (ms_out) *ms_out = ms;
+            if (prefetched_out) *prefetched_out = moved ? 1 : 0;
+        }
+        return rc;
     });
 }
 

@@ -11,6 +11,7 @@
 
 #include "spmm/bsr.h"
 #include "spmm/csr.h"
+#include "spmm/spmm_hybrid.h"
 
 namespace spmm {
 namespace engine {
@@ -78,6 +79,16 @@ Error build_bsr_device(const CSR& d_A, BSR* out, hipStream_t stream);
 // Fill-in statistics of a device CSR (the numbers bsr_compute_stats gives
 // for bsr_from_csr_host of the same matrix), without building the values.
 Error bsr_stats_device(const CSR& d_A, BSR_stats* out, hipStream_t stream);
+
+// Host-in/host-out execution of a hybrid plan (spmm_hybrid_run): *ms is the
+// median per-launch kernel time.
+Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float* h_C, int N,
+                 int warmup, int iters, float* ms);
+
+// Unified-memory execution (spmm_unified): *prefetched is false when the
+// device could not prefetch the managed ranges.
+Error run_unified(const CSR& h_A, const float* h_B, float* h_C, int N, int warmup, int iters,
+                  float* ms, bool* prefetched);
 
 // Number of workgroups the engine uses for an explicit partition of this CSR.
 int default_partition_parts(int num_rows, int nnz);

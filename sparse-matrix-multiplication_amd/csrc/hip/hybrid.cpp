@@ -2,41 +2,16 @@
 
 #include "spmm/spmm_hybrid.h"
 
+#include <cstdio>
+#include <cstdlib>
 #include <vector>
 
 #include "engine.h"
+#include "hip_status.h"
 #include "spmm/bsr.h"
-#include "spmm/metrics.h"
 #include "spmm/partition.h"
-#include "spmm/utils.h"
 
 namespace spmm {
-
-namespace {
-
-void exit_on_error(const engine::Error& e, const char* who) {
-    if (e.status == engine::kOk) return;
-    std::fprintf(stderr, "%s: %s\n", who, e.message.c_str());
-    std::exit(EXIT_FAILURE);
-}
-
-// warmup untimed launches, then iters launches each bracketed by events.
-template <typename Launch>
-float time_median_ms(Launch launch, int warmup, int iters) {
-    for (int i = 0; i < warmup; ++i) launch();
-    HIP_CHECK(hipDeviceSynchronize());
-    std::vector<float> times(static_cast<size_t>(iters > 0 ? iters : 0));
-    GpuTimer timer;
-    for (int i = 0; i < iters; ++i) {
-        timer.start();
-        launch();
-        timer.stop();
-        times[i] = timer.elapsed_ms();
-    }
-    return median(times);
-}
-
-}  // namespace
 
 const char* backend_name(Backend b) { return b == Backend::TENSOR_WMMA ? "wmma" : "csr"; }
 
@@ -62,71 +37,148 @@ HybridPlan hybrid_choose(const CSR& h_A, int N, float fill_in_threshold) {
     return plan;
 }
 
-float spmm_hybrid_run(const HybridPlan& plan, const CSR& h_A, const float* h_B, float* h_C,
-                      int N, int warmup, int iters) {
+namespace engine {
+
+namespace {
+
+// Device copy of a host CSR whose arrays free themselves.
+struct DeviceCsrCopy {
+    CSR          view;
+    DeviceBuffer rp, ci, va;
+};
+
+Error upload_csr(const CSR& h, DeviceCsrCopy& d) {
+    d.view = CSR{};
+    d.view.num_rows = h.num_rows;
+    d.view.num_cols = h.num_cols;
+    d.view.nnz      = h.nnz;
+    const size_t rp = sizeof(int) * (static_cast<size_t>(h.num_rows) + 1);
+    const size_t nz = static_cast<size_t>(h.nnz > 0 ? h.nnz : 1);
+    SPMM_TRY_HIP(hipMalloc(&d.rp.p, rp), "hipMalloc");
+    SPMM_TRY_HIP(hipMalloc(&d.ci.p, sizeof(int) * nz), "hipMalloc");
+    SPMM_TRY_HIP(hipMalloc(&d.va.p, sizeof(float) * nz), "hipMalloc");
+    SPMM_TRY_HIP(hipMemcpy(d.rp.p, h.row_ptr, rp, hipMemcpyHostToDevice), "hipMemcpy");
+    if (h.nnz > 0) {
+        SPMM_TRY_HIP(hipMemcpy(d.ci.p, h.col_idx, sizeof(int) * h.nnz, hipMemcpyHostToDevice),
+                     "hipMemcpy");
+        SPMM_TRY_HIP(hipMemcpy(d.va.p, h.values, sizeof(float) * h.nnz, hipMemcpyHostToDevice),
+                     "hipMemcpy");
+    }
+    d.view.row_ptr = d.rp.as<int>();
+    d.view.col_idx = d.ci.as<int>();
+    d.view.values  = d.va.as<float>();
+    return Error{};
+}
+
+// Device BSR (built on the device, or uploaded from a host build) that frees
+// its arrays.
+struct DeviceBsrCopy {
+    BSR view;
+    ~DeviceBsrCopy() {
+        if (view.row_ptr) (void)hipFree(view.row_ptr);
+        if (view.col_idx) (void)hipFree(view.col_idx);
+        if (view.values) (void)hipFree(view.values);
+    }
+};
+
+Error upload_bsr(const BSR_host& h, DeviceBsrCopy& d) {
+    d.view = BSR{};
+    d.view.num_rows   = h.num_rows;
+    d.view.num_cols   = h.num_cols;
+    d.view.block_rows = h.block_rows;
+    d.view.block_cols = h.block_cols;
+    d.view.num_blocks = h.num_blocks;
+    d.view.nnz        = h.nnz;
+    const size_t rp = sizeof(int) * h.row_ptr.size();
+    const size_t nb = static_cast<size_t>(h.num_blocks > 0 ? h.num_blocks : 1);
+    SPMM_TRY_HIP(hipMalloc(&d.view.row_ptr, rp), "hipMalloc");
+    SPMM_TRY_HIP(hipMalloc(&d.view.col_idx, sizeof(int) * nb), "hipMalloc");
+    SPMM_TRY_HIP(hipMalloc(&d.view.values, sizeof(half) * 256 * nb), "hipMalloc");
+    SPMM_TRY_HIP(hipMemcpy(d.view.row_ptr, h.row_ptr.data(), rp, hipMemcpyHostToDevice),
+                 "hipMemcpy");
+    if (h.num_blocks > 0) {
+        SPMM_TRY_HIP(hipMemcpy(d.view.col_idx, h.col_idx.data(), sizeof(int) * h.num_blocks,
+                               hipMemcpyHostToDevice), "hipMemcpy");
+        SPMM_TRY_HIP(hipMemcpy(d.view.values, h.values.data(), sizeof(half) * h.values.size(),
+                               hipMemcpyHostToDevice), "hipMemcpy");
+    }
+    return Error{};
+}
+
+}  // namespace
+
+Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float* h_C, int N,
+                 int warmup, int iters, float* ms) {
+    *ms = 0.f;
     const int M = h_A.num_rows;
     const int K = h_A.num_cols;
     const size_t b_elems = static_cast<size_t>(K) * N;
     const size_t c_elems = static_cast<size_t>(M) * N;
-    if (c_elems == 0) return 0.f;
+    if (c_elems == 0) return Error{};
 
-    float* d_B = nullptr;
-    float* d_C = nullptr;
-    HIP_CHECK(hipMalloc(&d_B, sizeof(float) * (b_elems > 0 ? b_elems : 1)));
-    HIP_CHECK(hipMalloc(&d_C, sizeof(float) * c_elems));
+    DeviceBuffer d_B, d_C;
+    SPMM_TRY_HIP(hipMalloc(&d_B.p, sizeof(float) * (b_elems > 0 ? b_elems : 1)), "hipMalloc");
+    SPMM_TRY_HIP(hipMalloc(&d_C.p, sizeof(float) * c_elems), "hipMalloc");
     if (b_elems > 0) {
-        HIP_CHECK(hipMemcpy(d_B, h_B, sizeof(float) * b_elems, hipMemcpyHostToDevice));
+        SPMM_TRY_HIP(hipMemcpy(d_B.p, h_B, sizeof(float) * b_elems, hipMemcpyHostToDevice),
+                     "hipMemcpy");
     }
 
-    float ms = 0.f;
     if (plan.backend == Backend::TENSOR_WMMA) {
         // Upload the CSR (8 bytes per nonzero; the BSR is 512 bytes per block)
         // and build the BSR on the device.  Inputs the device builder does not
         // take (rows with descending column indices, num_cols > 4128768) are
         // built on the host as in the reference (spmm_hybrid.cu:78-80).
-        BSR d_bsr;
+        DeviceBsrCopy bsr;
         {
-            CSR d_A = csr_to_device(h_A);
-            const engine::Error built = engine::build_bsr_device(d_A, &d_bsr, nullptr);
-            csr_free_device(d_A);
-            if (built.status == engine::kUnsupported) {
-                d_bsr = bsr_to_device(bsr_from_csr_host(h_A));
-            } else {
-                exit_on_error(built, "spmm_hybrid_run");
+            DeviceCsrCopy csr;
+            SPMM_TRY(upload_csr(h_A, csr));
+            const Error built = build_bsr_device(csr.view, &bsr.view, nullptr);
+            if (built.status == kUnsupported) {
+                SPMM_TRY(upload_bsr(bsr_from_csr_host(h_A), bsr));
+            } else if (built.status != kOk) {
+                return built;
             }
         }
-        half* d_B16 = nullptr;
-        HIP_CHECK(hipMalloc(&d_B16, sizeof(half) * (b_elems > 0 ? b_elems : 1)));
-        exit_on_error(engine::launch_float_to_half(d_B, d_B16, static_cast<long>(b_elems), nullptr),
-                      "spmm_hybrid_run");
-        HIP_CHECK(hipDeviceSynchronize());
-        ms = time_median_ms(
-            [&] { exit_on_error(engine::launch_bsr(d_bsr, d_B16, d_C, N, nullptr), "spmm_hybrid_run"); },
-            warmup, iters);
-        HIP_CHECK(hipFree(d_B16));
-        bsr_free_device(d_bsr);
+        DeviceBuffer d_B16;
+        SPMM_TRY_HIP(hipMalloc(&d_B16.p, sizeof(half) * (b_elems > 0 ? b_elems : 1)), "hipMalloc");
+        SPMM_TRY(launch_float_to_half(d_B.as<float>(), d_B16.as<half>(),
+                                      static_cast<long>(b_elems), nullptr));
+        SPMM_TRY(time_median_launch(
+            [&] { return launch_bsr(bsr.view, d_B16.as<half>(), d_C.as<float>(), N, nullptr); },
+            warmup, iters, ms));
     } else {
-        CSR d_A = csr_to_device(h_A);
-        const int parts = engine::default_partition_parts(M, h_A.nnz);
+        DeviceCsrCopy csr;
+        SPMM_TRY(upload_csr(h_A, csr));
+        const int parts = default_partition_parts(M, h_A.nnz);
         const std::vector<int> bounds = nnz_balanced_bounds(h_A, parts);
-        int* d_bounds = nullptr;
-        HIP_CHECK(hipMalloc(&d_bounds, sizeof(int) * bounds.size()));
-        HIP_CHECK(hipMemcpy(d_bounds, bounds.data(), sizeof(int) * bounds.size(),
-                            hipMemcpyHostToDevice));
-        ms = time_median_ms(
+        DeviceBuffer d_bounds;
+        SPMM_TRY_HIP(hipMalloc(&d_bounds.p, sizeof(int) * bounds.size()), "hipMalloc");
+        SPMM_TRY_HIP(hipMemcpy(d_bounds.p, bounds.data(), sizeof(int) * bounds.size(),
+                               hipMemcpyHostToDevice), "hipMemcpy");
+        SPMM_TRY(time_median_launch(
             [&] {
-                exit_on_error(engine::launch_csr(engine::CsrRole::TiledV3, d_A, d_B, d_C, N, nullptr,
-                                                 d_bounds, parts),
-                              "spmm_hybrid_run");
+                return launch_csr(CsrRole::TiledV3, csr.view, d_B.as<float>(), d_C.as<float>(), N,
+                                  nullptr, d_bounds.as<int>(), parts);
             },
-            warmup, iters);
-        HIP_CHECK(hipFree(d_bounds));
-        csr_free_device(d_A);
+            warmup, iters, ms));
     }
-    HIP_CHECK(hipDeviceSynchronize());
-    HIP_CHECK(hipMemcpy(h_C, d_C, sizeof(float) * c_elems, hipMemcpyDeviceToHost));
-    HIP_CHECK(hipFree(d_B));
-    HIP_CHECK(hipFree(d_C));
+    SPMM_TRY_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    SPMM_TRY_HIP(hipMemcpy(h_C, d_C.p, sizeof(float) * c_elems, hipMemcpyDeviceToHost),
+                 "hipMemcpy");
+    return Error{};
+}
+
+}  // namespace engine
+
+float spmm_hybrid_run(const HybridPlan& plan, const CSR& h_A, const float* h_B, float* h_C,
+                      int N, int warmup, int iters) {
+    float ms = 0.f;
+    const engine::Error e = engine::run_hybrid(plan, h_A, h_B, h_C, N, warmup, iters, &ms);
+    if (e.status != engine::kOk) {
+        std::fprintf(stderr, "spmm_hybrid_run: %s\n", e.message.c_str());
+        std::exit(EXIT_FAILURE);
+    }
     return ms;
 }
 

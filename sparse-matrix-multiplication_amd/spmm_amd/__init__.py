@@ -105,6 +105,8 @@ _SIGNATURES = {
     "spmm_c_bsr_from_csr_device": (_int, [_P(CsrT), _P(BsrT), _vp]),
     "spmm_c_bsr_stats_from_csr_device": (_int, [_P(CsrT), _P(BsrStatsT), _vp]),
     "spmm_c_bsr_to_host": (_int, [_P(BsrT), _P(BsrT)]),
+    "spmm_c_gpu_count": (_int, []),
+    "spmm_c_unified": (_int, [_P(CsrT), _vp, _vp, _int, _int, _int, _P(_float), _P(_int)]),
     "spmm_c_generate_power_law_csr": (_int, [_int, _int, _double, _double, _int, _int, _P(CsrT)]),
     "spmm_c_round_to_fp16": (_int, [_vp, _long]),
     "spmm_c_nnz_balanced_bounds": (_int, [_P(CsrT), _int, _vp]),
@@ -434,6 +436,25 @@ def hybrid_choose(m: HostCSR, N: int, threshold: Optional[float] = None) -> Plan
 
 def backend_name(backend: int) -> str:
     return lib().spmm_c_backend_name(backend).decode()
+
+
+def gpu_count() -> int:
+    """Reference spmm_multigpu.h:32."""
+    return int(lib().spmm_c_gpu_count())
+
+
+def unified_run(m: HostCSR, B: np.ndarray, warmup: int = 3, iters: int = 10):
+    """Reference spmm_unified (spmm_multigpu.cu:122-182): host in, host out ->
+    (C, median ms, prefetched)."""
+    B = np.ascontiguousarray(B, dtype=np.float32)
+    N = B.shape[1]
+    C = np.empty((m.num_rows, N), dtype=np.float32)
+    ms = ctypes.c_float()
+    moved = ctypes.c_int()
+    src = m.struct()
+    _check(lib().spmm_c_unified(ctypes.byref(src), _ptr(B), _ptr(C), N, warmup, iters,
+                                ctypes.byref(ms), ctypes.byref(moved)))
+    return C, ms.value, bool(moved.value)
 
 
 def hybrid_run(plan: Plan, m: HostCSR, B: np.ndarray, warmup: int = 3, iters: int = 10):

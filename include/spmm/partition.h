@@ -15,4 +15,11 @@ namespace spmm {
 
 std::vector<int> nnz_balanced_bounds(const CSR& h_A, int parts);
 
+// Row table of the merge-path (nonzero-split) partition used by the CSR
+// engine: part g covers nonzeros [nnz*g/parts, nnz*(g+1)/parts) (64-bit); rows[g]
+// is the row holding nonzero nnz*g/parts (the last row r < num_rows with
+// row_ptr[r] <= that index), rows[0] = 0, rows[parts] = num_rows.  Rows may be
+// split between parts.  Requires nnz >= 1.
+std::vector<int> nnz_split_rows(const CSR& h_A, int parts);
+
 }  // namespace spmm

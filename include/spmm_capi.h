@@ -100,6 +100,8 @@ typedef struct spmm_bsr_opts_t {
     int per_wave;  /* 1: wave kernel whatever row_group says */
     int depth;     /* wave kernel: block pairs in flight per wave: 1, 2, 4 */
     int xcd_order; /* wave kernel: 0, 1 XCD-grouped workgroup order; 2 dispatch order */
+    int rows;      /* wave kernel: block-rows per wave sharing staged B tiles: 1, 2, 4 */
+    int split;     /* wave kernel: 4 = the four waves of a workgroup split one block-row */
 } spmm_bsr_opts_t;
 
 const char* spmm_c_last_error(void);
@@ -175,13 +177,22 @@ int spmm_c_tiled_v3(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
                     void* stream);                               /* spmm_tiled_v3.h:40  */
 int spmm_c_tiled_v4(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
                     void* stream);                               /* spmm_tiled_v4.h:79  */
-/* spmm_tiled_v3 with an explicit nnz-balanced partition: d_bounds holds
- * parts+1 row bounds (spmm_c_nnz_balanced_bounds); used by spmm_hybrid_run
- * (spmm_hybrid.cu:103-116 launches spmm_tiled_v3 there). */
+/* spmm_tiled_v3 with an explicit nnz-balanced row partition: d_bounds holds
+ * parts+1 row bounds (spmm_c_nnz_balanced_bounds, the reference's split of
+ * spmm_multigpu.cu:26-40 applied to workgroups). */
 int spmm_c_tiled_v3_partitioned(const spmm_csr_t* d_A, const int* d_bounds, int parts,
                                 const float* d_B, float* d_C, int N, void* stream);
 /* Default number of parts for spmm_c_tiled_v3_partitioned. */
 int spmm_c_default_partition_parts(int num_rows, int nnz);
+/* Merge-path partition (no counterpart in the reference; used by spmm_hybrid_run):
+ * part g multiplies nonzeros [nnz*g/parts, nnz*(g+1)/parts), cutting long rows
+ * between workgroups.  d_split_rows: parts+1 ints from spmm_c_nnz_split_rows;
+ * d_carry: a workspace of parts * N floats.  Two launches (the engine, then
+ * the carry fix-up); results are deterministic. */
+int spmm_c_nnz_split_rows(const spmm_csr_t* h, int parts, int* h_rows_out);
+int spmm_c_split_partition_parts(int nnz);
+int spmm_c_tiled_v3_split(const spmm_csr_t* d_A, const int* d_split_rows, int parts,
+                          const float* d_B, float* d_C, int N, float* d_carry, void* stream);
 /* spmm_tiled_v3 with explicit engine options (no reference counterpart). */
 int spmm_c_tiled_v3_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
                          const spmm_engine_opts_t* opts, void* stream);
@@ -219,6 +230,9 @@ int spmm_c_hybrid_run(const spmm_hybrid_plan_t* plan, const spmm_csr_t* h_A,
 int spmm_c_launch_repeat(int kernel_id, const void* d_A_any, const void* d_B, float* d_C,
                          int N, int reps, void* stream);
 /* Same with explicit engine options for kernel id 5 (tiled_v3). */
+int spmm_c_launch_repeat_split(const spmm_csr_t* d_A, const int* d_split_rows, int parts,
+                               const float* d_B, float* d_C, int N, float* d_carry, int reps,
+                               void* stream);
 int spmm_c_launch_repeat_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
                               const spmm_engine_opts_t* opts, int reps, void* stream);
 /* Same for the matrix-core kernel with explicit options. */

@@ -260,6 +260,362 @@ __global__ __launch_bounds__(256) void bsr_wave_kernel(BsrArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Multi-row wave kernel: one wave = R consecutive block-rows x 16*J columns.
+// The wave walks the union of the R block-rows' (sorted) block-column lists
+// with R scalar cursors; every union pair's 32 B rows are loaded and staged
+// in LDS once and feed R MFMAs (one per block-row, zero A where a block-row
+// has no block at that column).  Neighbouring block-rows of banded and
+// block-diagonal matrices share most block-columns, so B traffic through the
+// CU and LDS falls by up to R without any workgroup barrier.
+//   - The R block-rows' blocks are contiguous in col_idx; when they total at
+//     most 64 they come in with one vector load and are merged in one
+//     segment.  Longer ones are taken block-row by block-row in chunks of 64
+//     (the other cursors empty).
+//   - The union cursor advances inside load_pair, so pairs are produced in
+//     order; loads are unconditional (exhausted cursors give masked loads of
+//     clamped valid addresses), as in the wave kernel.
+// ---------------------------------------------------------------------------
+template <int R, int J, int D, bool VEC>
+struct MultirowWave {
+    static constexpr int NT  = 16 * J;
+    static constexpr int S   = NT + 16;
+    static constexpr int CH  = NT / 8;
+    static constexpr int CPL = 32 * CH / 64;
+    static constexpr int kNone = 0x7fffffff;
+
+    struct PairRegs {
+        f16x8 b[CPL];
+        f16x8 af[R];
+        bool  b_ok[CPL];
+        bool  a_ok[R];
+        bool  valid;  // wave-uniform: the pair holds at least one union element
+    };
+
+    const BsrArgs& a;
+    _Float16*      tile;
+    int            lane, g, t, n0;
+    f32x4          acc[R][J];
+    // Current segment: lanes [0, cnt) of ci hold col_idx[base + lane]; list r
+    // (block-row r) is lanes [cur[r], end[r]).
+    int            base, ci;
+    int            cur[R], end[R];
+
+    __device__ MultirowWave(const BsrArgs& args, _Float16* t_, int n0_) : a(args), tile(t_), n0(n0_) {
+        lane = threadIdx.x & 63;
+        g    = lane >> 4;
+        t    = lane & 15;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int j = 0; j < J; ++j) acc[r][j] = f32x4(0.0f);
+        }
+    }
+
+    // Next union element: its block-column (-1 when the lists are exhausted)
+    // and, per block-row, its block index (-1 where the block-row has none).
+    __device__ void next_union(int& bc, int (&blk)[R]) {
+        int c[R];
+        int m = kNone;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int v = __builtin_amdgcn_readlane(ci, min(cur[r], 63));
+            c[r] = cur[r] < end[r] ? v : kNone;
+            m = min(m, c[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const bool has = m != kNone && c[r] == m;
+            blk[r] = has ? base + cur[r] : -1;
+            cur[r] += has ? 1 : 0;
+        }
+        bc = m == kNone ? -1 : m;
+    }
+
+    __device__ void load_pair(PairRegs& rg) {
+        int bc0, bc1, blk0[R], blk1[R];
+        next_union(bc0, blk0);
+        next_union(bc1, blk1);
+        rg.valid = bc0 >= 0;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = lane + c * 64;
+            const int s   = idx / CH;
+            const int bc  = s < 16 ? bc0 : bc1;
+            const int k   = bc * 16 + (s & 15);
+            const int n   = n0 + (idx % CH) * 8;
+            const bool ok = bc >= 0 && k < a.K && n < a.N;
+            rg.b_ok[c] = ok;
+            if constexpr (VEC) {
+                const size_t off = ok ? static_cast<size_t>(k) * a.N + n : 0;
+                rg.b[c] = *reinterpret_cast<const f16x8*>(a.B + off);
+            } else {
+                const size_t row = ok ? static_cast<size_t>(k) * a.N : 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const bool in = ok && n + e < a.N;
+                    const _Float16 x = a.B[in ? row + n + e : 0];
+                    rg.b[c][e] = in ? x : static_cast<_Float16>(0.0f);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int blk = g < 2 ? blk0[r] : blk1[r];
+            rg.a_ok[r] = blk >= 0;
+            rg.af[r] = *reinterpret_cast<const f16x8*>(
+                a.vals + static_cast<size_t>(blk >= 0 ? blk : base) * 256 + t * 16 + 8 * (g & 1));
+        }
+    }
+
+    __device__ void multiply(const PairRegs& rg) {
+        const f16x8 zero = f16x8(static_cast<_Float16>(0.0f));
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = lane + c * 64;
+            *reinterpret_cast<f16x8*>(&tile[(idx / CH) * S + (idx % CH) * 8]) =
+                rg.b_ok[c] ? rg.b[c] : zero;
+        }
+        const _Float16* rowp = &tile[(8 * g + (t >> 2)) * S + 4 * (t & 3)];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const s16x4 lo = lds_read_tr16(rowp + 16 * j);
+            const s16x4 hi = lds_read_tr16(rowp + 4 * S + 16 * j);
+            const s16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            const f16x8 bop = __builtin_bit_cast(f16x8, both);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const f16x8 af = rg.a_ok[r] ? rg.af[r] : zero;
+                acc[r][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bop, acc[r][j], 0, 0, 0);
+            }
+        }
+    }
+
+    // Walks the union of the current segment's lists.  Every slot of the ring
+    // is refilled unconditionally after its turn, so each iteration issues
+    // the same loads and the wait before a multiply covers only that slot.
+    // The union comes out in order: once slot 0 holds no union element, no
+    // later pair does.
+    __device__ void run_segment(int base_, int cnt) {
+        base = base_;
+        ci = lane < cnt ? a.col_idx[base + lane] : 0;
+        PairRegs ring[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) load_pair(ring[d]);
+        while (ring[0].valid) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                if (ring[d].valid) multiply(ring[d]);
+                load_pair(ring[d]);
+                // keep the slots' loads in issue order (the memory counter
+                // retires in order): a slot's wait then covers only its own
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+
+    __device__ void store(int br0) {
+        // D layout: lane holds rows 4*g + i, column t of each 16-column tile.
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int br = br0 + r;
+            if (br >= a.block_rows) break;
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int col = n0 + 16 * j + t;
+                if (col >= a.N) continue;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = br * 16 + 4 * g + i;
+                    if (row < a.M) a.C[static_cast<size_t>(row) * a.N + col] = acc[r][j][i];
+                }
+            }
+        }
+    }
+};
+
+template <int R, int J, int D, bool VEC>
+__global__ __launch_bounds__(256) void bsr_multirow_kernel(BsrArgs a) {
+    constexpr int S = 16 * J + 16;
+    __shared__ __attribute__((aligned(16))) _Float16 s_b[4][32 * S];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int bx, by;
+    wave_tile_of(a, bx, by);
+    const int br0 = (bx * 4 + wave) * R;
+    if (br0 >= a.block_rows) return;  // waves are independent: no barrier anywhere
+    MultirowWave<R, J, D, VEC> w(a, s_b[wave], by * 16 * J);
+
+    int rp[R + 1];
+#pragma unroll
+    for (int r = 0; r <= R; ++r) rp[r] = a.row_ptr[min(br0 + r, a.block_rows)];
+    const int tot = rp[R] - rp[0];
+    if (tot <= 64) {
+        // the R block-rows' blocks are contiguous: one segment, all lists
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            w.cur[r] = rp[r] - rp[0];
+            w.end[r] = rp[r + 1] - rp[0];
+        }
+        if (tot > 0) w.run_segment(rp[0], tot);
+    } else {
+        // block-row by block-row in chunks of 64 blocks (other lists empty)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            for (int c0 = rp[r]; c0 < rp[r + 1]; c0 += 64) {
+                const int cnt = min(64, rp[r + 1] - c0);
+#pragma unroll
+                for (int q = 0; q < R; ++q) {
+                    w.cur[q] = 0;
+                    w.end[q] = q == r ? cnt : 0;
+                }
+                w.run_segment(c0, cnt);
+            }
+        }
+    }
+    w.store(br0);
+}
+
+// ---------------------------------------------------------------------------
+// Split-K wave kernel: a workgroup of 4 waves owns one block-row x 16*J
+// columns; wave w multiplies the block pairs p = w, w+4, w+8, ... of the
+// block-row (pairs of consecutive blocks, as in the wave kernel), so each
+// wave's dependent chain is a quarter as long and four times as many waves
+// are in flight.  The four partial tiles are summed through LDS after one
+// workgroup barrier; wave w adds rows 4w .. 4w+3 of the tile and stores them.
+// ---------------------------------------------------------------------------
+template <int J, int D, bool VEC>
+__global__ __launch_bounds__(256) void bsr_splitk_kernel(BsrArgs a) {
+    constexpr int NT  = 16 * J;
+    constexpr int S   = NT + 16;
+    constexpr int CH  = NT / 8;
+    constexpr int CPL = 32 * CH / 64;
+    __shared__ __attribute__((aligned(16))) _Float16 s_b[4][32 * S];
+    __shared__ float s_part[4][16][NT + 1];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g    = lane >> 4;
+    const int t    = lane & 15;
+    int bx, by;
+    wave_tile_of(a, bx, by);
+    const int br = bx;  // grid = block_rows x column tiles: always a valid block-row
+    const int n0 = by * NT;
+    _Float16* tile = s_b[wave];
+    const int bs = a.row_ptr[br];
+    const int be = a.row_ptr[br + 1];
+
+    f32x4 acc[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) acc[j] = f32x4(0.0f);
+
+    struct PairRegs {
+        f16x8 b[CPL];
+        f16x8 af;
+        bool  b_ok[CPL];
+        bool  a_ok;
+    };
+    // pair q of the chunk = blocks 2q and 2q+1 of chunk ci (which starts at block base)
+    auto load_pair = [&](int base, int q, int cnt, int ci, PairRegs& r) {
+        const int p = min(2 * q, cnt - 1);  // clamped past the end: masked below
+        const bool live = 2 * q < cnt;
+        const bool two = live && p + 1 < cnt;
+        const int bc0 = __builtin_amdgcn_readlane(ci, p);
+        const int bc1 = __builtin_amdgcn_readlane(ci, two ? p + 1 : p);
+        const int blk = base + p;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = lane + c * 64;
+            const int s   = idx / CH;
+            const int k   = (s < 16 ? bc0 : bc1) * 16 + (s & 15);
+            const int n   = n0 + (idx % CH) * 8;
+            const bool ok = live && (s < 16 || two) && k < a.K && n < a.N;
+            r.b_ok[c] = ok;
+            if constexpr (VEC) {
+                const size_t off = ok ? static_cast<size_t>(k) * a.N + n : 0;
+                r.b[c] = *reinterpret_cast<const f16x8*>(a.B + off);
+            } else {
+                const size_t row = ok ? static_cast<size_t>(k) * a.N : 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const bool in = ok && n + e < a.N;
+                    const _Float16 x = a.B[in ? row + n + e : 0];
+                    r.b[c][e] = in ? x : static_cast<_Float16>(0.0f);
+                }
+            }
+        }
+        r.a_ok = live && (g < 2 || two);
+        r.af = *reinterpret_cast<const f16x8*>(
+            a.vals + static_cast<size_t>(blk + (r.a_ok ? (g >> 1) : 0)) * 256 + t * 16 +
+            8 * (g & 1));
+    };
+    auto multiply = [&](const PairRegs& r) {
+        const f16x8 zero = f16x8(static_cast<_Float16>(0.0f));
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = lane + c * 64;
+            *reinterpret_cast<f16x8*>(&tile[(idx / CH) * S + (idx % CH) * 8]) =
+                r.b_ok[c] ? r.b[c] : zero;
+        }
+        const f16x8 af = r.a_ok ? r.af : zero;
+        const _Float16* rowp = &tile[(8 * g + (t >> 2)) * S + 4 * (t & 3)];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const s16x4 lo = lds_read_tr16(rowp + 16 * j);
+            const s16x4 hi = lds_read_tr16(rowp + 4 * S + 16 * j);
+            const s16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(f16x8, both),
+                                                             acc[j], 0, 0, 0);
+        }
+    };
+
+    for (int c0 = bs; c0 < be; c0 += 64) {
+        const int cnt = min(64, be - c0);
+        const int np  = (cnt + 1) >> 1;
+        const int mine = np > wave ? (np - wave + 3) >> 2 : 0;  // pairs wave, wave+4, ...
+        if (mine == 0) continue;
+        const int ci = lane < cnt ? a.col_idx[c0 + lane] : 0;
+        PairRegs ring[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) load_pair(c0, wave + 4 * d, cnt, ci, ring[d]);
+        int i0 = 0;
+        for (; i0 + 2 * D <= mine; i0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                multiply(ring[d]);
+                load_pair(c0, wave + 4 * (i0 + d + D), cnt, ci, ring[d]);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (i0 + d < mine) {
+                multiply(ring[d]);
+                if (i0 + d + D < mine) load_pair(c0, wave + 4 * (i0 + d + D), cnt, ci, ring[d]);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (i0 + D + d < mine) multiply(ring[d]);
+        }
+    }
+
+    // Partial tiles -> LDS (lane holds rows 4g+i, column 16j+t), one barrier,
+    // then wave w sums rows 4w .. 4w+3 over the four partials.
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_part[wave][4 * g + i][16 * j + t] = acc[j][i];
+    }
+    __syncthreads();
+    for (int e = lane; e < 4 * NT; e += 64) {
+        const int lr  = 4 * wave + e / NT;
+        const int col = e % NT;
+        const float v = s_part[0][lr][col] + s_part[1][lr][col] + s_part[2][lr][col] +
+                        s_part[3][lr][col];
+        const int row = br * 16 + lr;
+        if (row < a.M && n0 + col < a.N) a.C[static_cast<size_t>(row) * a.N + n0 + col] = v;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Row-group kernel.
 //
 // A workgroup of RG waves owns RG consecutive block-rows (one per wave) and
@@ -493,6 +849,49 @@ hipError_t dispatch_wave(int depth, const BsrArgs& args, hipStream_t stream) {
                       : (depth == 2 ? run_wave<J, 2>(args, stream) : run_wave<J, 4>(args, stream));
 }
 
+template <int R, int J, int D>
+hipError_t run_multirow(BsrArgs args, hipStream_t stream) {
+    args.tiles_n = ceil_div(args.N, 16 * J);
+    const long total = static_cast<long>(ceil_div(args.block_rows, 4 * R)) * args.tiles_n;
+    if (total > 0x7fffffffL) return hipErrorInvalidConfiguration;
+    args.wg_total = static_cast<int>(total);
+    dim3 grid(args.wg_total);
+    if (args.b_vec_ok) {
+        hipLaunchKernelGGL((bsr_multirow_kernel<R, J, D, true>), grid, dim3(256), 0, stream, args);
+    } else {
+        hipLaunchKernelGGL((bsr_multirow_kernel<R, J, D, false>), grid, dim3(256), 0, stream, args);
+    }
+    return hipGetLastError();
+}
+
+template <int J, int D>
+hipError_t run_splitk(BsrArgs args, hipStream_t stream) {
+    args.tiles_n = ceil_div(args.N, 16 * J);
+    const long total = static_cast<long>(args.block_rows) * args.tiles_n;
+    if (total > 0x7fffffffL) return hipErrorInvalidConfiguration;
+    args.wg_total = static_cast<int>(total);
+    dim3 grid(args.wg_total);
+    if (args.b_vec_ok) {
+        hipLaunchKernelGGL((bsr_splitk_kernel<J, D, true>), grid, dim3(256), 0, stream, args);
+    } else {
+        hipLaunchKernelGGL((bsr_splitk_kernel<J, D, false>), grid, dim3(256), 0, stream, args);
+    }
+    return hipGetLastError();
+}
+
+hipError_t dispatch_splitk(int j, int depth, const BsrArgs& args, hipStream_t stream) {
+    if (j == 1) return depth == 1 ? run_splitk<1, 1>(args, stream) : run_splitk<1, 2>(args, stream);
+    if (j == 2) return depth == 1 ? run_splitk<2, 1>(args, stream) : run_splitk<2, 2>(args, stream);
+    return depth == 1 ? run_splitk<4, 1>(args, stream) : run_splitk<4, 2>(args, stream);
+}
+
+template <int R>
+hipError_t dispatch_multirow(int j, int depth, const BsrArgs& args, hipStream_t stream) {
+    if (j == 1) return depth == 1 ? run_multirow<R, 1, 1>(args, stream) : run_multirow<R, 1, 2>(args, stream);
+    if (j == 2) return depth == 1 ? run_multirow<R, 2, 1>(args, stream) : run_multirow<R, 2, 2>(args, stream);
+    return depth == 1 ? run_multirow<R, 4, 1>(args, stream) : run_multirow<R, 4, 2>(args, stream);
+}
+
 template <int RG, int J>
 hipError_t run_rowgroup(const BsrArgs& args, hipStream_t stream) {
     dim3 grid(ceil_div(args.block_rows, RG), ceil_div(args.N, 16 * J));
@@ -576,6 +975,16 @@ Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t strea
         // and the block-diagonal (c4, N = 256) configs.
         const int j = (o.tiles == 1 || o.tiles == 2 || o.tiles == 4) ? o.tiles : (N <= 16 ? 1 : 2);
         const int d = (o.depth == 1 || o.depth == 2 || o.depth == 4) ? o.depth : 2;
+        if (o.split == 4) {
+            e = dispatch_splitk(j, d == 1 ? 1 : 2, args, stream);
+            return from_hip(e, "spmm_wmma launch");
+        }
+        if (o.rows == 2 || o.rows == 4) {
+            const int dm = d == 1 ? 1 : 2;
+            e = o.rows == 2 ? dispatch_multirow<2>(j, dm, args, stream)
+                            : dispatch_multirow<4>(j, dm, args, stream);
+            return from_hip(e, "spmm_wmma launch");
+        }
         e = j == 1 ? dispatch_wave<1>(d, args, stream)
                    : (j == 2 ? dispatch_wave<2>(d, args, stream) : dispatch_wave<4>(d, args, stream));
         return from_hip(e, "spmm_wmma launch");

@@ -508,6 +508,15 @@ int spmm_c_nnz_balanced_bounds(const spmm_csr_t* h, int parts, int* out) {
     });
 }
 
+int spmm_c_nnz_split_rows(const spmm_csr_t* h, int parts, int* out) {
+    if (h == nullptr || out == nullptr) return set_error(SPMM_INVALID, "null argument");
+    return guarded([&] {
+        const std::vector<int> r = spmm::nnz_split_rows(to_cpp(*h), parts);
+        std::memcpy(out, r.data(), sizeof(int) * r.size());
+        return ok();
+    });
+}
+
 int spmm_c_compare(const float* ours, const float* ref, long n, float* max_abs, float* max_rel,
                    float* rel_l2) {
     if (n < 0 || (n > 0 && (ours == nullptr || ref == nullptr))) {
@@ -572,6 +581,19 @@ int spmm_c_default_partition_parts(int num_rows, int nnz) {
     return spmm::engine::default_partition_parts(num_rows, nnz);
 }
 
+int spmm_c_tiled_v3_split(const spmm_csr_t* d_A, const int* d_split_rows, int parts,
+                          const float* d_B, float* d_C, int N, float* d_carry, void* stream) {
+    if (d_A == nullptr || d_split_rows == nullptr) return set_error(SPMM_INVALID, "null argument");
+    spmm::engine::SplitPlan plan;
+    plan.rows  = d_split_rows;
+    plan.parts = parts;
+    plan.carry = d_carry;
+    return from_engine(spmm::engine::launch_csr_split(to_cpp(*d_A), d_B, d_C, N,
+                                                      as_stream(stream), plan));
+}
+
+int spmm_c_split_partition_parts(int nnz) { return spmm::engine::split_partition_parts(nnz); }
+
 int spmm_c_tiled_v3_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
                          const spmm_engine_opts_t* opts, void* stream) {
     if (d_A == nullptr) return set_error(SPMM_INVALID, "null argument");
@@ -600,6 +622,8 @@ int spmm_c_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B16, float* d_C,
         o.per_wave  = opts->per_wave;
         o.depth     = opts->depth;
         o.xcd_order = opts->xcd_order;
+        o.rows      = opts->rows;
+        o.split     = opts->split;
     }
     return from_engine(spmm::engine::launch_bsr(to_cpp(*d_bsr),
                                                 reinterpret_cast<const half*>(d_B16), d_C, N,
@@ -707,6 +731,23 @@ int spmm_c_launch_repeat_opts(const spmm_csr_t* d_A, const float* d_B, float* d_
     for (int i = 0; i < reps; ++i) {
         const int rc = from_engine(spmm::engine::launch_csr(
             spmm::engine::CsrRole::TiledV3, A, d_B, d_C, N, as_stream(stream), nullptr, 0, &o));
+        if (rc != SPMM_OK) return rc;
+    }
+    return ok();
+}
+
+int spmm_c_launch_repeat_split(const spmm_csr_t* d_A, const int* d_split_rows, int parts,
+                               const float* d_B, float* d_C, int N, float* d_carry, int reps,
+                               void* stream) {
+    if (d_A == nullptr || d_split_rows == nullptr) return set_error(SPMM_INVALID, "null argument");
+    spmm::engine::SplitPlan plan;
+    plan.rows  = d_split_rows;
+    plan.parts = parts;
+    plan.carry = d_carry;
+    const spmm::CSR A = to_cpp(*d_A);
+    for (int i = 0; i < reps; ++i) {
+        const int rc = from_engine(
+            spmm::engine::launch_csr_split(A, d_B, d_C, N, as_stream(stream), plan));
         if (rc != SPMM_OK) return rc;
     }
     return ok();

@@ -99,6 +99,10 @@ __global__ __launch_bounds__(256, MIN_WAVES_PER_EU) void csr_wave_per_row(
 // (an explicit nnz-balanced partition).  Inside the workgroup the nonzeros of
 // those rows are cut into WAVES equal contiguous ranges, one per wave, so a
 // long row is shared by several waves and many short rows by one wave.
+// Merge-path mode (split_rows) cuts at the workgroup level too: workgroup g
+// takes nonzeros [nnz*g/P, nnz*(g+1)/P) whatever rows they belong to; a row
+// that began in an earlier workgroup is summed into carry[g] instead of C, and
+// csr_split_fixup adds the carries to C in part order afterwards.
 //
 // Lane groups.  A wave is split into G groups of 64/G lanes; each group covers
 // one column tile of COLS = (64/G) * VEC columns with VEC-float (up to 16-byte)
@@ -139,6 +143,14 @@ struct RowblockArgs {
     int          nblocks;      // row blocks (workgroups of one column slice)
     int          slices;       // column slices: 1, 2, 4 or 8
     int          slice_cols;   // columns per slice (a multiple of VEC)
+    // Merge-path partition (nullable split_rows): part g = nonzeros
+    // [nnz*g/nblocks, nnz*(g+1)/nblocks); split_rows[g] is the row holding the
+    // first of them (split_rows[0] = 0, split_rows[nblocks] = M); carry is a
+    // nblocks x N workspace for the partial of a part's first row when that
+    // row began in an earlier part.
+    const int*   split_rows;
+    float*       carry;
+    long long    nnz;
 };
 
 constexpr int kRpCap = 1024;
@@ -217,13 +229,25 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
     const int cbeg = slice * a.slice_cols;
     const int cend = min(N, cbeg + a.slice_cols);
 
-    int r_begin, r_end;
-    if (a.bounds != nullptr) {
-        r_begin = a.bounds[rb];
-        r_end   = a.bounds[rb + 1];
+    int r_begin, r_end, zero_end;
+    const bool split = a.split_rows != nullptr;
+    long long nz_lo = 0, nz_hi = 0;
+    int wg_head = -1;  // first row, when it began in an earlier part (merge-path only)
+    if (split) {
+        nz_lo    = a.nnz * rb / a.nblocks;
+        nz_hi    = a.nnz * (rb + 1) / a.nblocks;
+        r_begin  = a.split_rows[rb];
+        zero_end = a.split_rows[rb + 1];          // empty rows [r_begin, zero_end) are ours
+        r_end    = min(a.M, zero_end + 1);         // + the row our last nonzeros start
+        if (nz_lo < nz_hi && r_begin < a.M && a.row_ptr[r_begin] < nz_lo) wg_head = r_begin;
+    } else if (a.bounds != nullptr) {
+        r_begin  = a.bounds[rb];
+        r_end    = a.bounds[rb + 1];
+        zero_end = r_end;
     } else {
-        r_begin = rb * a.rows_per_block;
-        r_end   = min(a.M, r_begin + a.rows_per_block);
+        r_begin  = rb * a.rows_per_block;
+        r_end    = min(a.M, r_begin + a.rows_per_block);
+        zero_end = r_end;
     }
 
     for (int w0 = r_begin; w0 < r_end; w0 += kRpCap) {
@@ -235,7 +259,7 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
         // Zero-fill the rows of this window that hold no nonzeros.
         for (int base = wave * kWave; base < nr; base += WAVES * kWave) {
             const int i = base + lane;
-            uint64_t empty = __ballot(i < nr && s_rp[i] == s_rp[i + 1]);
+            uint64_t empty = __ballot(i < nr && w0 + i < zero_end && s_rp[i] == s_rp[i + 1]);
             while (empty) {
                 const int b = __builtin_ctzll(empty);
                 empty &= empty - 1;
@@ -246,9 +270,14 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
             }
         }
 
-        const int nz0 = s_rp[0];
-        const int total = s_rp[nr] - nz0;
-        if (total == 0) continue;  // uniform across the workgroup
+        int nz0 = s_rp[0];
+        int nz_end = s_rp[nr];
+        if (split) {
+            nz0    = static_cast<int>(max(static_cast<long long>(nz0), nz_lo));
+            nz_end = static_cast<int>(min(static_cast<long long>(nz_end), nz_hi));
+        }
+        const int total = nz_end - nz0;
+        if (total <= 0) continue;  // uniform across the workgroup
         const int pa = nz0 + static_cast<int>((static_cast<long long>(total) * wave) / WAVES);
         const int pb = nz0 + static_cast<int>((static_cast<long long>(total) * (wave + 1)) / WAVES);
 
@@ -364,8 +393,47 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
                 }
                 if (writer) store_vec<VEC>(a.C + static_cast<size_t>(w0 + owner_row) * N + col, acc);
             }
+            if (wg_head >= 0 && w0 == r_begin && wave == 0) {
+                // The part's first row began in an earlier part: the waves that
+                // hold pieces of it (local row 0, leading waves) go to the carry.
+                VT sum = vzero<VEC>();
+                for (int w = 0; w < WAVES; ++w) {
+                    const int f = s_first[w];
+                    if (f == -2) continue;
+                    if (f != 0) break;
+                    sum += s_part[w][glane];
+                }
+                if (writer) store_vec<VEC>(a.carry + static_cast<size_t>(rb) * N + col, sum);
+            }
             __syncthreads();  // s_part / s_first are rewritten by the next column pass
         }
+    }
+}
+
+// Merge-path fix-up: row r that continues into parts g0+1 .. g1 was stored by
+// the part where it starts; the first continuation part adds the carries of
+// parts g0+1 .. g1 in part order (deterministic) to C[r].
+__global__ __launch_bounds__(256) void csr_split_fixup(const int* __restrict__ row_ptr,
+                                                       const int* __restrict__ split_rows,
+                                                       const float* __restrict__ carry,
+                                                       float* __restrict__ C, int M, int N,
+                                                       long long nnz, int parts) {
+    auto head_row = [&](int q) -> int {
+        const long long lo = nnz * q / parts;
+        const long long hi = nnz * (q + 1) / parts;
+        const int r = split_rows[q];
+        return (lo < hi && r < M && row_ptr[r] < lo) ? r : -1;
+    };
+    const int g = blockIdx.x;
+    const int r = head_row(g);
+    if (r < 0) return;
+    if (g > 0 && head_row(g - 1) == r) return;  // not the first continuation of row r
+    int last = g;
+    while (last + 1 < parts && head_row(last + 1) == r) ++last;
+    for (int c = threadIdx.x; c < N; c += blockDim.x) {
+        float s = 0.f;
+        for (int q = g; q <= last; ++q) s += carry[static_cast<size_t>(q) * N + c];
+        C[static_cast<size_t>(r) * N + c] += s;
     }
 }
 
@@ -447,8 +515,11 @@ int default_partition_parts(int num_rows, int nnz) {
     return static_cast<int>(std::max<long>(parts, 1));
 }
 
-Error launch_csr(CsrRole role, const CSR& A, const float* B, float* C, int N,
-                 hipStream_t stream, const int* bounds, int parts, const EngineOpts* opts) {
+namespace {
+
+Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int N,
+                      hipStream_t stream, const int* bounds, int parts, const EngineOpts* opts,
+                      const SplitPlan* split) {
     if (A.num_rows < 0 || A.num_cols < 0 || A.nnz < 0 || N < 0) {
         return fail(kInvalid, "negative matrix dimension");
     }
@@ -524,8 +595,14 @@ Error launch_csr(CsrRole role, const CSR& A, const float* B, float* C, int N,
     const int unroll = o.unroll == 16 ? 16 : 8;
 
     RowblockArgs args{A.row_ptr, A.col_idx, A.values, B, C, bounds, M, N, 0, 0, slices,
-                      slice_cols};
-    if (bounds != nullptr) {
+                      slice_cols, nullptr, nullptr, 0};
+    if (split != nullptr) {
+        args.bounds     = nullptr;
+        args.split_rows = split->rows;
+        args.carry      = split->carry;
+        args.nnz        = A.nnz;
+        args.nblocks    = split->parts;
+    } else if (bounds != nullptr) {
         args.nblocks = parts;
     } else {
         int rpb = o.rows_per_block;
@@ -547,7 +624,48 @@ Error launch_csr(CsrRole role, const CSR& A, const float* B, float* C, int N,
     } else {
         e = dispatch_groups<1>(groups, waves, unroll, args, grid, stream);
     }
+    if (e == hipSuccess && split != nullptr) {
+        hipLaunchKernelGGL(csr_split_fixup, dim3(split->parts), dim3(256), 0, stream, A.row_ptr,
+                           split->rows, split->carry, C, M, N, static_cast<long long>(A.nnz),
+                           split->parts);
+        e = hipGetLastError();
+    }
     return from_hip(e, "csr engine launch");
+}
+
+}  // namespace
+
+Error launch_csr(CsrRole role, const CSR& A, const float* B, float* C, int N,
+                 hipStream_t stream, const int* bounds, int parts, const EngineOpts* opts) {
+    return launch_csr_impl(role, A, B, C, N, stream, bounds, parts, opts, nullptr);
+}
+
+int split_partition_parts(int nnz) {
+    // Two workgroups per CU: measured on MI355X over power-law inputs of 0.6 M
+    // to 2.5 M nonzeros, 256 .. 1536 parts are within 10% of each other and
+    // 4096 parts lose 15-40% to per-workgroup set-up and the fix-up; more
+    // parts only for very large inputs (at most 64 K nonzeros per part).
+    long parts = std::max<long>(512, (static_cast<long>(nnz) + 65535) / 65536);
+    return static_cast<int>(std::min<long>(parts, std::max(nnz, 1)));
+}
+
+bool split_pays(int max_row_nnz) {
+    // A row longer than four default workgroups' share (4 x 640 nonzeros)
+    // keeps one row-partitioned workgroup busy long after the others: then the
+    // merge-path partition wins (power-law 8192^2: 51 -> 28 us; 16384^2: 125
+    // -> 104 us); on rows of similar length it costs its second launch (5-50%).
+    return max_row_nnz > 4 * 640;
+}
+
+Error launch_csr_split(const CSR& A, const float* B, float* C, int N, hipStream_t stream,
+                       const SplitPlan& plan, const EngineOpts* opts) {
+    if (plan.parts < 1 || plan.rows == nullptr) {
+        return fail(kInvalid, "split partition needs parts >= 1 and its row table");
+    }
+    if (plan.carry == nullptr && N > 0 && A.num_rows > 0) {
+        return fail(kInvalid, "split partition needs a carry workspace of parts x N floats");
+    }
+    return launch_csr_impl(CsrRole::TiledV3, A, B, C, N, stream, nullptr, 0, opts, &plan);
 }
 
 }  // namespace engine

@@ -66,6 +66,8 @@ struct BsrOpts {
     int per_wave  = 0;  // 1: wave kernel whatever row_group says
     int depth     = 0;  // wave kernel: block pairs in flight per wave, 1, 2 or 4
     int xcd_order = 0;  // wave kernel: 0, 1 XCD-grouped workgroup order; 2 dispatch order
+    int rows      = 0;  // wave kernel: block-rows per wave sharing staged B tiles, 1, 2 or 4
+    int split     = 0;  // wave kernel: 4 = the four waves of a workgroup split one block-row
 };
 
 Error launch_bsr(const BSR& d_A, const half* d_B, float* d_C, int N, hipStream_t stream,
@@ -89,6 +91,25 @@ Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float
 // device could not prefetch the managed ranges.
 Error run_unified(const CSR& h_A, const float* h_B, float* h_C, int N, int warmup, int iters,
                   float* ms, bool* prefetched);
+
+// Merge-path partition of the row-block engine: part g takes nonzeros
+// [nnz*g/P, nnz*(g+1)/P) whatever rows they belong to, so a long row is shared
+// by several workgroups.  rows (P+1 device ints, nnz_split_rows) holds the row
+// of each part's first nonzero; carry is a device workspace of P x N floats.
+// The part where a row starts stores it; later parts holding pieces of it
+// write their partial to carry, and a second kernel adds those to C in part
+// order (deterministic).
+struct SplitPlan {
+    const int* rows  = nullptr;
+    int        parts = 0;
+    float*     carry = nullptr;
+};
+Error launch_csr_split(const CSR& d_A, const float* d_B, float* d_C, int N, hipStream_t stream,
+                       const SplitPlan& plan, const EngineOpts* opts = nullptr);
+// Parts of the merge-path partition for nnz nonzeros, and whether it beats
+// the row partition for a matrix whose longest row has max_row_nnz entries.
+int split_partition_parts(int nnz);
+bool split_pays(int max_row_nnz);
 
 // Number of workgroups the engine uses for an explicit partition of this CSR.
 int default_partition_parts(int num_rows, int nnz);

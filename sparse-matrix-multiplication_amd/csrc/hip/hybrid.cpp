@@ -2,6 +2,7 @@
 
 #include "spmm/spmm_hybrid.h"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <vector>
@@ -148,20 +149,42 @@ Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float
             [&] { return launch_bsr(bsr.view, d_B16.as<half>(), d_C.as<float>(), N, nullptr); },
             warmup, iters, ms));
     } else {
+        // The reference launches spmm_tiled_v3 over all rows
+        // (spmm_hybrid.cu:103-116).  Rows much longer than a workgroup's share
+        // (power-law inputs) would leave their workgroups running long after
+        // the rest, so then the engine runs the merge-path partition instead:
+        // equal nonzero ranges per workgroup, long rows cut between them.
         DeviceCsrCopy csr;
         SPMM_TRY(upload_csr(h_A, csr));
-        const int parts = default_partition_parts(M, h_A.nnz);
-        const std::vector<int> bounds = nnz_balanced_bounds(h_A, parts);
-        DeviceBuffer d_bounds;
-        SPMM_TRY_HIP(hipMalloc(&d_bounds.p, sizeof(int) * bounds.size()), "hipMalloc");
-        SPMM_TRY_HIP(hipMemcpy(d_bounds.p, bounds.data(), sizeof(int) * bounds.size(),
-                               hipMemcpyHostToDevice), "hipMemcpy");
-        SPMM_TRY(time_median_launch(
-            [&] {
-                return launch_csr(CsrRole::TiledV3, csr.view, d_B.as<float>(), d_C.as<float>(), N,
-                                  nullptr, d_bounds.as<int>(), parts);
-            },
-            warmup, iters, ms));
+        int max_row = 0;
+        for (int r = 0; r < M; ++r) max_row = std::max(max_row, h_A.row_ptr[r + 1] - h_A.row_ptr[r]);
+        if (h_A.nnz == 0 || !split_pays(max_row)) {
+            SPMM_TRY(time_median_launch(
+                [&] {
+                    return launch_csr(CsrRole::TiledV3, csr.view, d_B.as<float>(),
+                                      d_C.as<float>(), N, nullptr);
+                },
+                warmup, iters, ms));
+        } else {
+            const int parts = split_partition_parts(h_A.nnz);
+            const std::vector<int> rows = nnz_split_rows(h_A, parts);
+            DeviceBuffer d_rows, d_carry;
+            SPMM_TRY_HIP(hipMalloc(&d_rows.p, sizeof(int) * rows.size()), "hipMalloc");
+            SPMM_TRY_HIP(hipMemcpy(d_rows.p, rows.data(), sizeof(int) * rows.size(),
+                                   hipMemcpyHostToDevice), "hipMemcpy");
+            SPMM_TRY_HIP(hipMalloc(&d_carry.p, sizeof(float) * static_cast<size_t>(parts) * N),
+                         "hipMalloc");
+            SplitPlan plan;
+            plan.rows  = d_rows.as<int>();
+            plan.parts = parts;
+            plan.carry = d_carry.as<float>();
+            SPMM_TRY(time_median_launch(
+                [&] {
+                    return launch_csr_split(csr.view, d_B.as<float>(), d_C.as<float>(), N, nullptr,
+                                            plan);
+                },
+                warmup, iters, ms));
+        }
     }
     SPMM_TRY_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
     SPMM_TRY_HIP(hipMemcpy(h_C, d_C.p, sizeof(float) * c_elems, hipMemcpyDeviceToHost),

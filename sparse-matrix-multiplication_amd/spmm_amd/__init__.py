@@ -72,7 +72,8 @@ class EngineOptsT(ctypes.Structure):
 
 class BsrOptsT(ctypes.Structure):
     _fields_ = [("row_group", ctypes.c_int), ("tiles", ctypes.c_int), ("per_wave", ctypes.c_int),
-                ("depth", ctypes.c_int), ("xcd_order", ctypes.c_int)]
+                ("depth", ctypes.c_int), ("xcd_order", ctypes.c_int), ("rows", ctypes.c_int),
+                ("split", ctypes.c_int)]
 
 
 _P = ctypes.POINTER
@@ -121,6 +122,10 @@ _SIGNATURES = {
     "spmm_c_tiled_v3": (_int, [_P(CsrT), _vp, _vp, _int, _vp]),
     "spmm_c_tiled_v4": (_int, [_P(CsrT), _vp, _vp, _int, _vp]),
     "spmm_c_tiled_v3_partitioned": (_int, [_P(CsrT), _vp, _int, _vp, _vp, _int, _vp]),
+    "spmm_c_nnz_split_rows": (_int, [_P(CsrT), _int, _vp]),
+    "spmm_c_split_partition_parts": (_int, [_int]),
+    "spmm_c_tiled_v3_split": (_int, [_P(CsrT), _vp, _int, _vp, _vp, _int, _vp, _vp]),
+    "spmm_c_launch_repeat_split": (_int, [_P(CsrT), _vp, _int, _vp, _vp, _int, _vp, _int, _vp]),
     "spmm_c_default_partition_parts": (_int, [_int, _int]),
     "spmm_c_tiled_v3_opts": (_int, [_P(CsrT), _vp, _vp, _int, _P(EngineOptsT), _vp]),
     "spmm_c_float_to_half": (_int, [_vp, _vp, _long, _vp]),
@@ -386,6 +391,18 @@ def default_partition_parts(num_rows: int, nnz: int) -> int:
     return int(lib().spmm_c_default_partition_parts(num_rows, nnz))
 
 
+def nnz_split_rows(m: HostCSR, parts: int) -> np.ndarray:
+    """Row table of the merge-path partition (parts + 1 ints)."""
+    out = np.empty(parts + 1, dtype=np.int32)
+    src = m.struct()
+    _check(lib().spmm_c_nnz_split_rows(ctypes.byref(src), parts, _ptr(out)))
+    return out
+
+
+def split_partition_parts(nnz: int) -> int:
+    return int(lib().spmm_c_split_partition_parts(nnz))
+
+
 def compare(ours: np.ndarray, ref: np.ndarray):
     """Reference harness.cu:179-196 -> (max_abs, max_rel, rel_l2)."""
     a = np.ascontiguousarray(ours, dtype=np.float32).ravel()
@@ -594,6 +611,31 @@ def spmm_tiled_v3_partitioned(A: DeviceCSR, bounds, B, C=None, stream=None):
                                              int(bounds.numel()) - 1, B.data_ptr(),
                                              C.data_ptr(), N, _stream_handle(stream)))
     return C
+
+
+def spmm_tiled_v3_split(A: DeviceCSR, split_rows, B, C=None, carry=None, stream=None):
+    """Merge-path partition: split_rows = cuda int32 tensor of parts+1 rows."""
+    torch = _torch()
+    N = int(B.shape[1])
+    parts = int(split_rows.numel()) - 1
+    if C is None:
+        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B.device)
+    if carry is None:
+        carry = torch.empty((max(parts, 1), max(N, 1)), dtype=torch.float32, device=B.device)
+    s = A.struct()
+    _check(lib().spmm_c_tiled_v3_split(ctypes.byref(s), split_rows.data_ptr(), parts,
+                                       B.data_ptr(), C.data_ptr(), N, carry.data_ptr(),
+                                       _stream_handle(stream)))
+    return C
+
+
+def launch_repeat_split(A: DeviceCSR, split_rows, B, C, carry, reps: int, stream=None) -> None:
+    """reps back-to-back merge-path launches (measurement helper)."""
+    s = A.struct()
+    _check(lib().spmm_c_launch_repeat_split(ctypes.byref(s), split_rows.data_ptr(),
+                                            int(split_rows.numel()) - 1, B.data_ptr(),
+                                            C.data_ptr(), int(B.shape[1]), carry.data_ptr(),
+                                            reps, _stream_handle(stream)))
 
 
 def spmm_tiled_v3_opts(A: DeviceCSR, B, opts: EngineOptsT, C=None, stream=None):

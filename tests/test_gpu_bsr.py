@@ -156,6 +156,102 @@ def test_wmma_chunk_boundaries(S, O, torch):
             check_csr(C, C64, absC, tol=1e-5)
 
 
+@pytest.mark.parametrize("rows", [2, 4])
+@pytest.mark.parametrize("tiles,depth", [(1, 1), (1, 2), (2, 1), (2, 2), (4, 1), (4, 2)])
+def test_wmma_multirow(S, O, torch, rows, tiles, depth):
+    # R block-rows per wave walking the union of their block-columns: banded
+    # and block-diagonal (shared columns), random (mostly disjoint), empty and
+    # ragged block-rows, block-row counts not divisible by 4R
+    cases = _cases(S)
+    for name in ("single_block", "odd_pair_count", "ragged_dims", "n_not_16", "n_1",
+                 "empty_block_rows", "empty", "wide_n", "block_diag_small"):
+        A, B = cases[name]
+        hb, B16, C32, C64, absC = _refs(S, O, A, B)
+        say(f"wmma multirow rows={rows} tiles={tiles} depth={depth} case={name}")
+        dC = torch.full((hb.num_rows, B16.shape[1]), float("nan"), device="cuda")
+        S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
+                         S.BsrOptsT(0, tiles, 0, depth, 0, rows), dC)
+        torch.cuda.synchronize()
+        C = dC.cpu().numpy()
+        check_bsr(C, C32, absC)
+        check_csr(C, C64, absC, tol=1e-5)
+
+
+@pytest.mark.parametrize("rows", [2, 4])
+def test_wmma_multirow_long_and_chunked(S, O, torch, rows):
+    # more than 64 blocks over the R block-rows (block-row by block-row in
+    # chunks of 64) next to groups that merge
+    rowsl, cols = [], []
+    for br, nb in enumerate((63, 64, 65, 128, 129, 1, 0, 2, 3, 5, 30, 31)):
+        for b in range(nb):
+            rowsl.append(br * 16 + (b % 16))
+            cols.append(((b * 7 + br) % 130) * 16 + (br % 16))
+    A = S.csr_from_coo_host(12 * 16, 130 * 16, np.array(rowsl), np.array(cols),
+                            np.random.default_rng(5).uniform(-1, 1, len(rowsl)).astype(np.float32))
+    A.values = S.round_to_fp16(A.values)
+    B = S.round_to_fp16(np.random.default_rng(6).uniform(-1, 1, (130 * 16, 48)).astype(np.float32))
+    hb, B16, C32, C64, absC = _refs(S, O, A, B)
+    for tiles in (1, 2, 4):
+        for depth in (1, 2):
+            say(f"wmma multirow chunks rows={rows} tiles={tiles} depth={depth}")
+            C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
+                                 S.BsrOptsT(0, tiles, 0, depth, 0, rows)).cpu().numpy()
+            check_bsr(C, C32, absC)
+            check_csr(C, C64, absC, tol=1e-5)
+
+
+@pytest.mark.parametrize("rows", [2, 4])
+@pytest.mark.parametrize("cfg", ["c3", "c4"])
+def test_wmma_multirow_configs(S, O, torch, rows, cfg):
+    A, B = make_config(S, cfg)
+    hb, B16, C32, C64, absC = _refs(S, O, A, B)
+    say(f"wmma multirow config={cfg} rows={rows}")
+    C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
+                         S.BsrOptsT(0, 0, 0, 0, 0, rows)).cpu().numpy()
+    check_bsr(C, C32, absC)
+    check_csr(C, C64, absC, tol=1e-5)
+
+
+@pytest.mark.parametrize("tiles,depth", [(1, 1), (1, 2), (2, 1), (2, 2), (4, 1), (4, 2)])
+def test_wmma_split(S, O, torch, tiles, depth):
+    # the four waves of a workgroup share one block-row (pairs w, w+4, ...)
+    # and add their partial tiles through LDS
+    cases = _cases(S)
+    for name in ("single_block", "odd_pair_count", "ragged_dims", "n_not_16", "n_1",
+                 "empty_block_rows", "empty", "wide_n", "block_diag_small"):
+        A, B = cases[name]
+        hb, B16, C32, C64, absC = _refs(S, O, A, B)
+        say(f"wmma split tiles={tiles} depth={depth} case={name}")
+        dC = torch.full((hb.num_rows, B16.shape[1]), float("nan"), device="cuda")
+        S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
+                         S.BsrOptsT(0, tiles, 0, depth, 0, 0, 4), dC)
+        torch.cuda.synchronize()
+        C = dC.cpu().numpy()
+        check_bsr(C, C32, absC)
+        check_csr(C, C64, absC, tol=1e-5)
+
+
+def test_wmma_split_chunks_and_configs(S, O, torch):
+    rowsl, cols = [], []
+    for br, nb in enumerate((63, 64, 65, 128, 129, 1, 0, 2, 3, 5, 7, 9)):
+        for b in range(nb):
+            rowsl.append(br * 16 + (b % 16))
+            cols.append(((b * 7 + br) % 130) * 16 + (br % 16))
+    A = S.csr_from_coo_host(12 * 16, 130 * 16, np.array(rowsl), np.array(cols),
+                            np.random.default_rng(5).uniform(-1, 1, len(rowsl)).astype(np.float32))
+    A.values = S.round_to_fp16(A.values)
+    B = S.round_to_fp16(np.random.default_rng(6).uniform(-1, 1, (130 * 16, 48)).astype(np.float32))
+    mats = [("chunks", A, B)] + [(c, *make_config(S, c)) for c in ("c3", "c4")]
+    for name, A, B in mats:
+        hb, B16, C32, C64, absC = _refs(S, O, A, B)
+        for tiles, depth in ((1, 2), (2, 1), (2, 2), (4, 2)):
+            say(f"wmma split {name} tiles={tiles} depth={depth}")
+            C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
+                                 S.BsrOptsT(0, tiles, 0, depth, 0, 0, 4)).cpu().numpy()
+            check_bsr(C, C32, absC)
+            check_csr(C, C64, absC, tol=1e-5)
+
+
 @pytest.mark.parametrize("xcd_order", [1, 2])
 def test_wmma_workgroup_orders(S, O, torch, xcd_order):
     # both workgroup -> tile maps of the wave kernel cover every tile once,

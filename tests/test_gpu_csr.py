@@ -193,6 +193,56 @@ def test_partitioned_engine(S, torch, edge_cases, config_refs, parts):
         check_csr(dC.cpu().numpy(), C64, absC)
 
 
+def _split_run(S, torch, A, B, parts):
+    rows = torch.from_numpy(S.nnz_split_rows(A, parts)).cuda()
+    dC = torch.full((A.num_rows, B.shape[1]), float("nan"), device="cuda")
+    S.spmm_tiled_v3_split(S.DeviceCSR(A), rows, torch.from_numpy(B).cuda(), dC)
+    torch.cuda.synchronize()
+    return dC.cpu().numpy()
+
+
+@pytest.mark.parametrize("parts", [1, 2, 7, 64, 513, 5000])
+def test_split_engine(S, torch, edge_cases, config_refs, parts):
+    # merge-path partition: equal nonzero ranges per workgroup, rows cut
+    # between workgroups and completed by the carry fix-up
+    names = ("ragged", "power_law_small", "identity", "k_is_1", "n1", "n3", "n17", "n96",
+             "n130", "n257", "n512", "one_by_one")
+    for name in names:
+        A, B, C64, absC = edge_cases[name]
+        p = max(1, min(parts, A.nnz))
+        say(f"csr split parts={p} case={name} M={A.num_rows} nnz={A.nnz} N={B.shape[1]}")
+        check_csr(_split_run(S, torch, A, B, p), C64, absC)
+    A, B, C64, absC = config_refs("c5")
+    say(f"csr split parts={parts} config=c5")
+    check_csr(_split_run(S, torch, A, B, parts), C64, absC)
+
+
+def test_split_engine_long_rows_and_empty_rows(S, O, torch):
+    # one row of 20000 entries spanning dozens of parts, empty rows on part
+    # boundaries and at both ends, a part of a single nonzero
+    rng = np.random.default_rng(21)
+    M, K, N = 300, 30000, 64
+    r = [5] * 20000 + list(rng.integers(10, 290, 3000)) + [299]
+    c = list(rng.permutation(K)[:20000]) + list(rng.integers(0, K, 3000)) + [7]
+    keep = [i for i in range(len(r)) if r[i] % 4 != 1]
+    A = S.csr_from_coo_host(M, K, np.array(r)[keep], np.array(c)[keep],
+                            rng.uniform(-1, 1, len(keep)).astype(np.float32))
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)
+    for parts in (3, 40, 333, A.nnz):
+        say(f"csr split long-row parts={parts} nnz={A.nnz}")
+        C1 = _split_run(S, torch, A, B, parts)
+        check_csr(C1, C64, absC)
+        C2 = _split_run(S, torch, A, B, parts)
+        assert np.array_equal(C1.view(np.uint32), C2.view(np.uint32))  # deterministic
+
+
+def test_split_engine_errors(S, torch):
+    s = S.CsrT(4, 4, 1, 0, 0, 0)
+    assert S.lib().spmm_c_tiled_v3_split(ctypes.byref(s), None, 1, 0, 0, 4, None, None) == \
+        S.SPMM_INVALID
+
+
 def test_tiled_v2_contract(S, torch, edge_cases):
     A, B, _, _ = edge_cases["n96"]
     dA = S.DeviceCSR(A)

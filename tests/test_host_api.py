@@ -233,3 +233,24 @@ def test_bsr_stats_from_csr_host_equals_full_build(S):
         for f in ("num_blocks", "stored_elements", "original_nnz", "fill_in_ratio",
                   "block_density"):
             assert getattr(fast, f) == getattr(full, f), f
+
+
+def test_nnz_split_rows_definition(S):
+    # rows[g] = last row r < M with row_ptr[r] <= nnz*g/parts; rows[0] = 0, rows[parts] = M
+    rng = np.random.default_rng(12)
+    mats = [S.generate_power_law_csr(500, 400, 20.0, 1.5, 400, 3),
+            S.csr_from_coo_host(50, 30, [3, 3, 3, 40, 41, 41], [0, 5, 9, 1, 2, 3], np.ones(6)),
+            S.csr_from_coo_host(20, 2000, np.full(1500, 7), rng.permutation(2000)[:1500],
+                                rng.uniform(-1, 1, 1500))]
+    for A in mats:
+        for parts in (1, 2, 3, 7, 64, A.nnz, A.nnz + 5):
+            rows = S.nnz_split_rows(A, parts)
+            assert rows[0] == 0 and rows[parts] == A.num_rows
+            assert np.all(np.diff(rows) >= 0)
+            for g in range(1, parts):
+                p = A.nnz * g // parts
+                want = max(r for r in range(A.num_rows) if A.row_ptr[r] <= p)
+                assert rows[g] == want, (g, p)
+                assert A.row_ptr[rows[g]] <= p < A.row_ptr[rows[g] + 1]  # the row holds p
+    with pytest.raises(S.SpmmError):
+        S.nnz_split_rows(S.csr_from_coo_host(4, 4, [], [], []), 3)

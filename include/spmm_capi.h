@@ -85,10 +85,12 @@ typedef struct spmm_hybrid_plan_t {
 typedef struct spmm_engine_opts_t {
     int vec;            /* floats per lane per B load: 1, 2, 4 */
     int waves;          /* waves per workgroup: 2, 4, 8 */
-    int unroll;         /* B row segments in flight per lane per step: 8, 16 */
+    int unroll;         /* B row segments per lane per step (two steps in flight): 4, 8 */
     int rows_per_block; /* implicit partition granularity */
     int groups;         /* lane groups per wave, entries interleaved: 1, 2, 4 */
     int slices;         /* XCD-tied column slices of B and C: 1, 2, 4, 8 */
+    int global_loads;   /* 1: 64-bit address loads of B instead of buffer loads
+                           (automatic when B exceeds 2 GiB or N > 4095) */
 } spmm_engine_opts_t;
 
 /* BSR matrix-core kernel tuning (0 = automatic).  No counterpart in the

@@ -150,6 +150,7 @@ spmm::engine::EngineOpts opts_from_c(const spmm_engine_opts_t* o) {
         e.rows_per_block = o->rows_per_block;
         e.groups         = o->groups;
         e.slices         = o->slices;
+        e.global_loads   = o->global_loads;
     }
     return e;
 }

@@ -15,6 +15,20 @@
 #include "engine.h"
 #include "spmm/utils.h"
 
+typedef float spmm_f32x2 __attribute__((ext_vector_type(2)));
+typedef float spmm_f32x4 __attribute__((ext_vector_type(4)));
+
+// Structured buffer loads (LLVM's AMDGPU intrinsics; index = record, offset =
+// byte offset inside the record).  The intrinsic names are fixed by LLVM.
+__device__ spmm_f32x4 sbuf_load_x4(__amdgpu_buffer_rsrc_t rsrc, int index, int offset,
+                                   int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.v4f32");
+__device__ spmm_f32x2 sbuf_load_x2(__amdgpu_buffer_rsrc_t rsrc, int index, int offset,
+                                   int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.v2f32");
+__device__ float sbuf_load_x1(__amdgpu_buffer_rsrc_t rsrc, int index, int offset, int soffset,
+                              int aux) __asm("llvm.amdgcn.struct.ptr.buffer.load.f32");
+
 namespace spmm {
 namespace engine {
 
@@ -109,15 +123,19 @@ __global__ __launch_bounds__(256, MIN_WAVES_PER_EU) void csr_wave_per_row(
 // loads, and the groups take interleaved entries of the wave's range (group h
 // takes entries h, h+G, h+2G, ...).  One load instruction therefore fetches G
 // different B row segments: for N = 128 fp32, G = 2 and each half-wave reads
-// one 512-byte row with dwordx4 loads, which is what the gfx950 vector memory
-// pipe serves fastest for random row gathers.
+// one 512-byte row with dwordx4 loads.
 //
-// Per wave.  The range is streamed in 64-entry chunks held in VGPRs (lane q
-// holds col_idx / value of entry q; the next chunk is prefetched while the
-// current one is consumed).  v_readlane broadcasts the entries of a step to
-// their groups, U row segments per lane are in flight per step, and every
-// lane accumulates into a VEC-wide register tile.  At a row boundary the
-// groups' tiles are summed with cross-lane shuffles and the row is flushed:
+// Per wave.  The wave copies (col, value) pairs of its range into its own LDS
+// window (kWCap entries, all loads issued at once); every lane then reads the
+// entry of its group with one broadcast ds_read_b64 and gathers its B segment
+// with a bounds-checked buffer load (one record per B row, so the row index is
+// the load's index operand and needs no address arithmetic).  The range is
+// walked in steps of U*G entries with the next step's loads in flight while
+// the current step is accumulated.  A scalar test per step sends only the
+// steps that cross a row end to the slow path, so row bookkeeping costs per
+// row, not per entry (measured on MI355X: per-entry scalar tests made the
+// kernel issue-bound on the shared scalar unit).  At a row end the groups'
+// tiles are summed with cross-lane shuffles and the row is flushed:
 //   - a row that lies wholly inside the wave's range is stored to C;
 //   - the first row of a range that started in an earlier wave goes to an LDS
 //     slot (s_part[wave]);
@@ -139,6 +157,7 @@ struct RowblockArgs {
     const int*   bounds;  // nullable
     int          M;
     int          N;
+    int          K;            // rows of B (records of the B buffer)
     int          rows_per_block;
     int          nblocks;      // row blocks (workgroups of one column slice)
     int          slices;       // column slices: 1, 2, 4 or 8
@@ -153,23 +172,31 @@ struct RowblockArgs {
     long long    nnz;
 };
 
-constexpr int kRpCap = 1024;
+constexpr int kRpCap = 1024;  // row pointers staged per window
+constexpr int kWCap  = 256;   // (col, value) entries a wave stages at a time
+
+// Third dword of a gfx9 buffer resource: 32-bit data format, no swizzle.
+constexpr int kBufWord3 = 0x00020000;
+
+// VEC floats of B row k at byte offset colb: a structured-buffer load (record
+// k of N*4 bytes; rows outside [0, K) read as zeros), or a plain 64-bit
+// address when B is too large for the buffer form.
+template <int VEC, bool SBUF>
+__device__ __forceinline__ typename Vec<VEC>::T load_b(__amdgpu_buffer_rsrc_t rsrc,
+                                                       const float* bcol, int k, int colb,
+                                                       int N) {
+    if constexpr (SBUF) {
+        if constexpr (VEC == 4) return sbuf_load_x4(rsrc, k, colb, 0, 0);
+        else if constexpr (VEC == 2) return sbuf_load_x2(rsrc, k, colb, 0, 0);
+        else return sbuf_load_x1(rsrc, k, colb, 0, 0);
+    } else {
+        return *reinterpret_cast<const typename Vec<VEC>::T*>(bcol + static_cast<size_t>(k) * N);
+    }
+}
 
 template <int VEC>
 __device__ __forceinline__ void store_vec(float* p, typename Vec<VEC>::T v) {
     __builtin_nontemporal_store(v, reinterpret_cast<typename Vec<VEC>::T*>(p));
-}
-
-// Value of x held by lane q + (this lane's group), for groups of 64/G lanes.
-template <int G>
-__device__ __forceinline__ int pick(int x, int q, int grp) {
-    int r = __builtin_amdgcn_readlane(x, q);
-#pragma unroll
-    for (int h = 1; h < G; ++h) {
-        const int t = __builtin_amdgcn_readlane(x, q + h);
-        r = grp == h ? t : r;
-    }
-    return r;
 }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m); }
@@ -196,17 +223,25 @@ __device__ __forceinline__ typename Vec<VEC>::T reduce_groups(typename Vec<VEC>:
     }
 }
 
-template <int VEC, int G, int WAVES, int U>
+// Orders a wave's LDS writes before its own lanes' reads of them.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int VEC, int G, int WAVES, int U, bool SBUF>
 __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
     using VT = typename Vec<VEC>::T;
     constexpr int LPG  = kWave / G;   // lanes per group
     constexpr int COLS = LPG * VEC;   // columns per pass
     constexpr int STEP = U * G;       // entries per step
-    static_assert(kWave % STEP == 0, "U * G must divide the wave size");
+    static_assert(kWave % STEP == 0 && kWCap % kWave == 0, "U * G must divide the wave size");
 
-    __shared__ int s_rp[kRpCap + 1];
-    __shared__ VT  s_part[WAVES][LPG];
-    __shared__ int s_first[WAVES];
+    __shared__ int  s_rp[kRpCap + 1];
+    __shared__ VT   s_part[WAVES][LPG];
+    __shared__ int  s_first[WAVES];
+    __shared__ int2 s_kv[WAVES][kWCap + STEP];
 
     const int lane  = threadIdx.x & (kWave - 1);
     const int wave  = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -250,6 +285,33 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
         zero_end = r_end;
     }
 
+    __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(a.B), static_cast<short>(SBUF ? N * 4 : 0), SBUF ? a.K : 0, kBufWord3);
+    // Entries past a window's end read by the masked lanes of its last step.
+    for (int i = lane; i < STEP; i += kWave) s_kv[wave][kWCap + i] = make_int2(0, 0);
+
+    // Copies entries [lo, hi) (hi - lo <= kWCap) into the wave's LDS window;
+    // the rest of the window holds (0, 0).  All loads are issued before the
+    // first LDS write.
+    auto stage = [&](int lo, int hi) {
+        constexpr int NL = kWCap / kWave;
+        int   kk[NL];
+        float vx[NL];
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int e = min(lo + i * kWave + lane, hi - 1);
+            kk[i] = a.col_idx[e];
+            vx[i] = a.vals[e];
+        }
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const bool in = lo + i * kWave + lane < hi;
+            s_kv[wave][i * kWave + lane] =
+                make_int2(in ? kk[i] : 0, in ? __builtin_bit_cast(int, vx[i]) : 0);
+        }
+        wave_lds_sync();
+    };
+
     for (int w0 = r_begin; w0 < r_end; w0 += kRpCap) {
         const int nr = min(r_end - w0, kRpCap);
         __syncthreads();  // the previous window is no longer read
@@ -292,19 +354,24 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
             first = lo;
         }
 
+        // A range that fits one window is staged once for all column passes.
+        const bool one_window = pb - pa <= kWCap;
+        if (one_window && pa < pb) stage(pa, pb);
+
         for (int c0 = cbeg; c0 < cend; c0 += COLS) {
             const int  col    = c0 + glane * VEC;
             const bool col_ok = col < cend;
             const int  col_ld = col_ok ? col : 0;  // loads stay in bounds; never stored
             const bool writer = grp == 0 && col_ok;
+            const float* bcol = a.B + col_ld;
             if (lane == 0) s_first[wave] = (pa < pb) ? -1 : -2;
 
             int owner_row = -1;  // local row this wave finishes after the barrier
             VT acc = vzero<VEC>();
             if (pa < pb) {
-                int  row      = first;
-                int  row_stop = s_rp[row + 1];
-                bool head     = s_rp[row] < pa;  // row began in an earlier wave
+                int  row     = first;
+                int  row_end = s_rp[row + 1];
+                bool head    = s_rp[row] < pa;  // row began in an earlier wave
 
                 auto flush = [&]() {
                     const VT t = reduce_groups<VEC, G>(acc);
@@ -318,63 +385,59 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
                     acc = vzero<VEC>();
                 };
 
-                int   kn = 0;
-                float vn = 0.f;
-                if (lane < min(kWave, pb - pa)) {
-                    kn = __builtin_nontemporal_load(a.col_idx + pa + lane);
-                    vn = __builtin_nontemporal_load(a.vals + pa + lane);
-                }
-                for (int base = pa; base < pb; base += kWave) {
-                    const int cnt = min(kWave, pb - base);
-                    const int   kc = kn;  // lanes >= cnt hold k = 0 (a valid B row), v = 0
-                    const float vc = vn;
-                    const int nb = base + kWave;
-                    if (nb < pb) {  // prefetch the next chunk
-                        kn = 0;
-                        vn = 0.f;
-                        if (lane < min(kWave, pb - nb)) {
-                            kn = __builtin_nontemporal_load(a.col_idx + nb + lane);
-                            vn = __builtin_nontemporal_load(a.vals + nb + lane);
-                        }
-                    }
-                    for (int j = 0; j < cnt; j += STEP) {
-                        VT    bv[U];
-                        float vv[U];
+                for (int win = pa; win < pb; win += kWCap) {
+                    const int win_end = min(pb, win + kWCap);
+                    if (!one_window) stage(win, win_end);
+
+                    VT    bA[U], bB[U];
+                    float vA[U], vB[U];
+                    // Loads of the step starting at entry q.
+                    auto issue = [&](VT (&bv)[U], float (&vv)[U], int q) {
 #pragma unroll
                         for (int u = 0; u < U; ++u) {
-                            const int q = j + u * G;
-                            const int k = pick<G>(kc, q, grp);
-                            vv[u] = __builtin_bit_cast(float, pick<G>(__builtin_bit_cast(int, vc), q, grp));
-                            bv[u] = *reinterpret_cast<const VT*>(a.B + static_cast<size_t>(k) * N + col_ld);
+                            const int2 kv = s_kv[wave][q - win + u * G + grp];
+                            vv[u] = __builtin_bit_cast(float, kv.y);
+                            bv[u] = load_b<VEC, SBUF>(rsrc, bcol, kv.x, col_ld * 4, N);
                         }
+                    };
+                    // Accumulates the step starting at entry q.
+                    auto consume = [&](VT (&bv)[U], float (&vv)[U], int q) {
+                        if (q + STEP <= row_end && q + STEP <= win_end) {
 #pragma unroll
-                        for (int u = 0; u < U; ++u) {
-                            const int q0 = j + u * G;
-                            const int p0 = base + q0;
-                            if (q0 + G <= cnt && p0 + G <= row_stop) {
-                                acc = vv[u] * bv[u] + acc;  // all G entries valid, same row
-                            } else {
+                            for (int u = 0; u < U; ++u) acc = vv[u] * bv[u] + acc;
+                        } else {
+#pragma unroll
+                            for (int u = 0; u < U; ++u) {
 #pragma unroll
                                 for (int h = 0; h < G; ++h) {
-                                    if (q0 + h >= cnt) break;  // past the end of the range
-                                    const int P = p0 + h;
-                                    if (P >= row_stop) {
-                                        flush();
-                                        // bounded by the window even for a malformed row_ptr
-                                        do {
-                                            ++row;
-                                            row_stop = s_rp[row + 1];
-                                        } while (row_stop <= P && row < nr - 1);
+                                    const int P = q + u * G + h;
+                                    if (P < win_end) {
+                                        if (P >= row_end) {
+                                            flush();
+                                            // bounded by the window even for a malformed row_ptr
+                                            do {
+                                                ++row;
+                                                row_end = s_rp[row + 1];
+                                            } while (row_end <= P && row < nr - 1);
+                                        }
+                                        if (grp == h) acc = vv[u] * bv[u] + acc;
                                     }
-                                    if (grp == h) acc = vv[u] * bv[u] + acc;
                                 }
                             }
                         }
+                    };
+                    issue(bA, vA, win);
+                    for (int q = win; q < win_end; q += 2 * STEP) {
+                        if (q + STEP < win_end) issue(bB, vB, q + STEP);
+                        consume(bA, vA, q);
+                        if (q + STEP >= win_end) break;
+                        if (q + 2 * STEP < win_end) issue(bA, vA, q + 2 * STEP);
+                        consume(bB, vB, q + STEP);
                     }
                 }
                 // The row being accumulated when the range ends.
                 acc = reduce_groups<VEC, G>(acc);
-                if (row_stop == pb && !head) {
+                if (row_end == pb && !head) {
                     if (writer) store_vec<VEC>(a.C + static_cast<size_t>(w0 + row) * N + col, acc);
                 } else if (head) {
                     if (grp == 0) s_part[wave][glane] = acc;
@@ -474,42 +537,52 @@ int pick_groups(int N, int vec, int want) {
     return 1;
 }
 
-template <int VEC, int G, int WAVES, int U>
+template <int VEC, int G, int WAVES, int U, bool SBUF>
 hipError_t run_rowblock(const RowblockArgs& args, int grid, hipStream_t stream) {
-    hipLaunchKernelGGL((csr_rowblock<VEC, G, WAVES, U>), dim3(grid), dim3(WAVES * kWave), 0,
+    hipLaunchKernelGGL((csr_rowblock<VEC, G, WAVES, U, SBUF>), dim3(grid), dim3(WAVES * kWave), 0,
                        stream, args);
     return hipGetLastError();
 }
 
+// Launch shapes: waves per workgroup (2, 4, 8) x entries in flight per lane
+// per step (4, 8).  B loads through a structured buffer unless B is too large
+// for one (then only the default shape, 8 waves x 4, is built).
 template <int VEC, int G>
-hipError_t dispatch_shape(int waves, int unroll, const RowblockArgs& args, int grid,
+hipError_t dispatch_shape(int waves, int unroll, bool sbuf, const RowblockArgs& args, int grid,
                           hipStream_t stream) {
+    if (!sbuf) return run_rowblock<VEC, G, 8, 4, false>(args, grid, stream);
     if (waves == 8) {
-        return unroll == 16 ? run_rowblock<VEC, G, 8, 16>(args, grid, stream)
-                            : run_rowblock<VEC, G, 8, 8>(args, grid, stream);
+        return unroll == 8 ? run_rowblock<VEC, G, 8, 8, true>(args, grid, stream)
+                           : run_rowblock<VEC, G, 8, 4, true>(args, grid, stream);
     }
     if (waves == 2) {
-        return unroll == 16 ? run_rowblock<VEC, G, 2, 16>(args, grid, stream)
-                            : run_rowblock<VEC, G, 2, 8>(args, grid, stream);
+        return unroll == 8 ? run_rowblock<VEC, G, 2, 8, true>(args, grid, stream)
+                           : run_rowblock<VEC, G, 2, 4, true>(args, grid, stream);
     }
-    return unroll == 16 ? run_rowblock<VEC, G, 4, 16>(args, grid, stream)
-                        : run_rowblock<VEC, G, 4, 8>(args, grid, stream);
+    return unroll == 8 ? run_rowblock<VEC, G, 4, 8, true>(args, grid, stream)
+                       : run_rowblock<VEC, G, 4, 4, true>(args, grid, stream);
 }
 
 template <int VEC>
-hipError_t dispatch_groups(int groups, int waves, int unroll, const RowblockArgs& args, int grid,
-                           hipStream_t stream) {
-    if (groups == 4) return dispatch_shape<VEC, 4>(waves, unroll, args, grid, stream);
-    if (groups == 2) return dispatch_shape<VEC, 2>(waves, unroll, args, grid, stream);
-    return dispatch_shape<VEC, 1>(waves, unroll, args, grid, stream);
+hipError_t dispatch_groups(int groups, int waves, int unroll, bool sbuf, const RowblockArgs& args,
+                           int grid, hipStream_t stream) {
+    if (groups == 4) return dispatch_shape<VEC, 4>(waves, unroll, sbuf, args, grid, stream);
+    if (groups == 2) return dispatch_shape<VEC, 2>(waves, unroll, sbuf, args, grid, stream);
+    return dispatch_shape<VEC, 1>(waves, unroll, sbuf, args, grid, stream);
 }
 
+// B rows as buffer records: the record stride field holds at most 16383
+// bytes and the buffer's byte range must fit a signed 32-bit offset.
+bool b_fits_buffer(int K, int N) {
+    return static_cast<long long>(N) * 4 <= 16383 &&
+           static_cast<long long>(K) * N * 4 <= 0x7fffffffLL;
+}
 }  // namespace
 
 int default_partition_parts(int num_rows, int nnz) {
-    // About 640 nonzeros per workgroup (80 per wave of the default 8-wave
+    // About 1280 nonzeros per workgroup (160 per wave of the default 8-wave
     // shape), at least two workgroups per CU and at most one per row.
-    long parts = (static_cast<long>(nnz) + 639) / 640;
+    long parts = (static_cast<long>(nnz) + 1279) / 1280;
     parts = std::max<long>(parts, 512);
     parts = std::min<long>(parts, std::max(num_rows, 1));
     return static_cast<int>(std::max<long>(parts, 1));
@@ -589,13 +662,15 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
     slice_cols = ceil_div(slice_cols, vec) * vec;
     const int groups = pick_groups(slice_cols, vec, want_groups);
     // Defaults measured on MI355X (c1 / c2 / c5 sweeps): 8 waves per
-    // workgroup, 8 row segments in flight per lane, about 80 nonzeros per wave
-    // and at least 512 workgroups (two per CU) when the matrix allows it.
+    // workgroup, 4 entries per group in flight per step (two steps in
+    // flight), about 160 nonzeros per wave and at least 512 workgroups (two
+    // per CU) when the matrix allows it.
     const int waves = (o.waves == 2 || o.waves == 4) ? o.waves : 8;
-    const int unroll = o.unroll == 16 ? 16 : 8;
+    const int unroll = o.unroll == 8 ? 8 : 4;
+    const bool sbuf = o.global_loads == 0 && b_fits_buffer(A.num_cols, N);
 
-    RowblockArgs args{A.row_ptr, A.col_idx, A.values, B, C, bounds, M, N, 0, 0, slices,
-                      slice_cols, nullptr, nullptr, 0};
+    RowblockArgs args{A.row_ptr, A.col_idx, A.values, B,       C,       bounds, M, N, A.num_cols,
+                      0,         0,         slices,   slice_cols, nullptr, nullptr, 0};
     if (split != nullptr) {
         args.bounds     = nullptr;
         args.split_rows = split->rows;
@@ -608,7 +683,7 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
         int rpb = o.rows_per_block;
         if (rpb <= 0) {
             const double avg = A.nnz > 0 ? static_cast<double>(A.nnz) / M : 1.0;
-            rpb = static_cast<int>(80.0 * waves / std::max(avg, 1.0) + 0.5);
+            rpb = static_cast<int>(160.0 * waves / std::max(avg, 1.0) + 0.5);
             rpb = std::min(rpb, M / 512);
         }
         rpb = std::max(1, std::min(rpb, kRpCap));
@@ -618,11 +693,11 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
     const int grid = slices == 1 ? args.nblocks : ceil_div(args.nblocks, 8 / slices) * 8;
     hipError_t e;
     if (vec == 4) {
-        e = dispatch_groups<4>(groups, waves, unroll, args, grid, stream);
+        e = dispatch_groups<4>(groups, waves, unroll, sbuf, args, grid, stream);
     } else if (vec == 2) {
-        e = dispatch_groups<2>(groups, waves, unroll, args, grid, stream);
+        e = dispatch_groups<2>(groups, waves, unroll, sbuf, args, grid, stream);
     } else {
-        e = dispatch_groups<1>(groups, waves, unroll, args, grid, stream);
+        e = dispatch_groups<1>(groups, waves, unroll, sbuf, args, grid, stream);
     }
     if (e == hipSuccess && split != nullptr) {
         hipLaunchKernelGGL(csr_split_fixup, dim3(split->parts), dim3(256), 0, stream, A.row_ptr,

@@ -38,10 +38,11 @@ enum class CsrRole : int {
 struct EngineOpts {
     int vec            = 0;  // floats per lane per B load: 1, 2 or 4
     int waves          = 0;  // waves per workgroup: 2, 4 or 8
-    int unroll         = 0;  // B-row loads in flight per lane per step: 8 or 16
+    int unroll         = 0;  // B-row loads per lane per step (two steps in flight): 4 or 8
     int rows_per_block = 0;  // implicit partition: rows per workgroup
     int groups         = 0;  // lane groups per wave (entries interleaved): 1, 2 or 4
     int slices         = 0;  // XCD-tied column slices of B and C: 1, 2, 4 or 8
+    int global_loads   = 0;  // 1: 64-bit address loads of B instead of buffer loads
 };
 
 struct Error {

@@ -134,12 +134,14 @@ def test_engine_deterministic(S, torch, config_refs):
 
 @pytest.mark.parametrize("vec", [1, 2, 4])
 @pytest.mark.parametrize("groups", [1, 2, 4])
-@pytest.mark.parametrize("waves,unroll", [(2, 16), (4, 8), (8, 16)])
-def test_engine_variants(S, torch, edge_cases, config_refs, vec, groups, waves, unroll):
-    opts = S.EngineOptsT(vec, waves, unroll, 0, groups)
+@pytest.mark.parametrize("waves,unroll,gl", [(2, 8, 0), (4, 4, 0), (8, 8, 0), (8, 4, 1)])
+def test_engine_variants(S, torch, edge_cases, config_refs, vec, groups, waves, unroll, gl):
+    # gl = 1: B through 64-bit address loads (the form used when B does not
+    # fit a buffer resource) instead of structured-buffer loads
+    opts = S.EngineOptsT(vec, waves, unroll, 0, groups, 0, gl)
     for name in ("ragged", "power_law_small", "n3", "n17", "n96", "n257", "n512", "empty_nnz"):
         A, B, C64, absC = edge_cases[name]
-        say(f"csr engine vec={vec} groups={groups} waves={waves} unroll={unroll} case={name}")
+        say(f"csr engine vec={vec} groups={groups} waves={waves} unroll={unroll} gl={gl} case={name}")
         dA = S.DeviceCSR(A)
         dB = torch.from_numpy(B).cuda()
         dC = torch.full((A.num_rows, B.shape[1]), float("nan"), device="cuda")
@@ -148,11 +150,11 @@ def test_engine_variants(S, torch, edge_cases, config_refs, vec, groups, waves, 
         check_csr(dC.cpu().numpy(), C64, absC)
     for rpb in (1, 7, 1024):
         A, B, C64, absC = edge_cases["ragged"]
-        say(f"csr engine vec={vec} groups={groups} waves={waves} unroll={unroll} rows_per_block={rpb}")
+        say(f"csr engine vec={vec} groups={groups} waves={waves} unroll={unroll} gl={gl} rows_per_block={rpb}")
         dA = S.DeviceCSR(A)
         dB = torch.from_numpy(B).cuda()
         dC = torch.full((A.num_rows, B.shape[1]), float("nan"), device="cuda")
-        S.spmm_tiled_v3_opts(dA, dB, S.EngineOptsT(vec, waves, unroll, rpb, groups), dC)
+        S.spmm_tiled_v3_opts(dA, dB, S.EngineOptsT(vec, waves, unroll, rpb, groups, 0, gl), dC)
         torch.cuda.synchronize()
         check_csr(dC.cpu().numpy(), C64, absC)
 
@@ -160,7 +162,7 @@ def test_engine_variants(S, torch, edge_cases, config_refs, vec, groups, waves, 
 @pytest.mark.parametrize("slices", [2, 4, 8])
 @pytest.mark.parametrize("vec", [0, 1])
 def test_engine_column_slices(S, torch, edge_cases, config_refs, slices, vec):
-    opts = S.EngineOptsT(vec, 8, 8, 0, 0, slices)
+    opts = S.EngineOptsT(vec, 8, 4, 0, 0, slices)
     for name in ("ragged", "power_law_small", "n1", "n3", "n17", "n96", "n130", "n257", "n512",
                  "empty_nnz", "identity"):
         A, B, C64, absC = edge_cases[name]

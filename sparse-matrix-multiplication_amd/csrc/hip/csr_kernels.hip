@@ -571,6 +571,19 @@ hipError_t dispatch_groups(int groups, int waves, int unroll, bool sbuf, const R
     return dispatch_shape<VEC, 1>(waves, unroll, sbuf, args, grid, stream);
 }
 
+// Column slices for a K x N fp32 B: the fewest (a power of two, at most 8,
+// each slice at least 64 columns wide) that bring one XCD's share of B down
+// to its 4 MiB L2.  Measured on MI355X: B of 8 MiB (16384 x 128, 8192 x 256)
+// 1.2-1.7x faster with 2 slices; B of 4 MiB or less is fastest unsliced.
+int auto_slices(int K, int N) {
+    const long long b_bytes = static_cast<long long>(K) * N * 4;
+    int s = 1;
+    while (s < 8 && b_bytes > (4LL << 20) * s && N / (2 * s) >= 64) s *= 2;
+    return s;
+}
+
+int default_waves(int slices) { return slices == 1 ? 8 : 4; }
+
 // B rows as buffer records: the record stride field holds at most 16383
 // bytes and the buffer's byte range must fit a signed 32-bit offset.
 bool b_fits_buffer(int K, int N) {
@@ -647,25 +660,20 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
         return fail(kInvalid, "engine vec must be 1, 2 or 4");
     }
     const int vec = pick_vec(N, B, C, want_vec);
-    // Column slices (XCD-aware, see the kernel): 1, 2, 4 or 8.  Automatic:
-    // one slice per 128 columns once B rows are wider than that, so each XCD
-    // gathers 512-byte row pieces of a B slice that fits its L2 (measured on
-    // MI355X: N = 256 -> 2 slices, 1.15-1.45x; N = 512 -> 4 slices, 1.5-1.7x;
-    // N = 128 -> 1, where slicing only shortens the gathers).
+    // Column slices (XCD-aware, see the kernel): 1, 2, 4 or 8.
     int slices = o.slices;
-    if (slices == 0 && vec == 4 && role != CsrRole::Tiled) {
-        slices = 1;
-        while (slices < 8 && N >= 256 * slices) slices *= 2;
-    }
+    if (slices == 0) slices = role == CsrRole::Tiled ? 1 : auto_slices(A.num_cols, N);
     if (slices != 1 && slices != 2 && slices != 4 && slices != 8) slices = 1;
     int slice_cols = ceil_div(N, slices);
     slice_cols = ceil_div(slice_cols, vec) * vec;
     const int groups = pick_groups(slice_cols, vec, want_groups);
-    // Defaults measured on MI355X (c1 / c2 / c5 sweeps): 8 waves per
-    // workgroup, 4 entries per group in flight per step (two steps in
-    // flight), about 160 nonzeros per wave and at least 512 workgroups (two
-    // per CU) when the matrix allows it.
-    const int waves = (o.waves == 2 || o.waves == 4) ? o.waves : 8;
+    // Defaults measured on MI355X (c1 / c2 / c5 and uniform / power-law
+    // sweeps): 8 waves per workgroup without column slices, 4 with them (the
+    // sliced launch has twice the workgroups per row block), 4 entries per
+    // group in flight per step (two steps in flight), about 160 nonzeros per
+    // wave and at least 512 workgroups (two per CU) when the matrix allows it.
+    const int waves = (o.waves == 2 || o.waves == 4 || o.waves == 8) ? o.waves
+                                                                     : default_waves(slices);
     const int unroll = o.unroll == 8 ? 8 : 4;
     const bool sbuf = o.global_loads == 0 && b_fits_buffer(A.num_cols, N);
 
@@ -725,10 +733,11 @@ int split_partition_parts(int nnz) {
 }
 
 bool split_pays(int max_row_nnz) {
-    // A row longer than four default workgroups' share (4 x 640 nonzeros)
-    // keeps one row-partitioned workgroup busy long after the others: then the
-    // merge-path partition wins (power-law 8192^2: 51 -> 28 us; 16384^2: 125
-    // -> 104 us); on rows of similar length it costs its second launch (5-50%).
+    // A row longer than four workgroups' share (4 x 640 nonzeros at 4 waves
+    // of 160) keeps one row-partitioned workgroup busy long after the others:
+    // then the merge-path partition wins (power-law 8192^2: 32 -> 23 us;
+    // 16384^2 with two column slices: 88 -> 69 us); on rows of similar length
+    // it costs its second launch (5-50%).
     return max_row_nnz > 4 * 640;
 }
 

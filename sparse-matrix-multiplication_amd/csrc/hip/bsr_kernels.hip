@@ -58,6 +58,10 @@ __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict
     }
 }
 
+// C is written once and not read back by the kernel: streaming stores keep
+// it from displacing A and B in L2 (measured on c4: 7.8 -> 7.5 us).
+__device__ __forceinline__ void store_c(float* p, float v) { __builtin_nontemporal_store(v, p); }
+
 struct BsrArgs {
     const int*      row_ptr;
     const int*      col_idx;
@@ -254,7 +258,7 @@ __global__ __launch_bounds__(256) void bsr_wave_kernel(BsrArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = br * 16 + 4 * g + i;
-            if (row < a.M) a.C[static_cast<size_t>(row) * a.N + col] = acc[j][i];
+            if (row < a.M) store_c(a.C + static_cast<size_t>(row) * a.N + col, acc[j][i]);
         }
     }
 }
@@ -426,7 +430,7 @@ struct MultirowWave {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int row = br * 16 + 4 * g + i;
-                    if (row < a.M) a.C[static_cast<size_t>(row) * a.N + col] = acc[r][j][i];
+                    if (row < a.M) store_c(a.C + static_cast<size_t>(row) * a.N + col, acc[r][j][i]);
                 }
             }
         }
@@ -611,7 +615,7 @@ __global__ __launch_bounds__(256) void bsr_splitk_kernel(BsrArgs a) {
         const float v = s_part[0][lr][col] + s_part[1][lr][col] + s_part[2][lr][col] +
                         s_part[3][lr][col];
         const int row = br * 16 + lr;
-        if (row < a.M && n0 + col < a.N) a.C[static_cast<size_t>(row) * a.N + n0 + col] = v;
+        if (row < a.M && n0 + col < a.N) store_c(a.C + static_cast<size_t>(row) * a.N + n0 + col, v);
     }
 }
 
@@ -815,7 +819,7 @@ __global__ __launch_bounds__(RG * 64) void bsr_rowgroup_kernel(BsrArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = br * 16 + 4 * g + i;
-                if (row < a.M) a.C[static_cast<size_t>(row) * a.N + col] = acc[j][i];
+                if (row < a.M) store_c(a.C + static_cast<size_t>(row) * a.N + col, acc[j][i]);
             }
         }
     }

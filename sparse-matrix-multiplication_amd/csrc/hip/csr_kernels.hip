@@ -527,11 +527,14 @@ int pick_vec(int N, const float* B, float* C, int want) {
     return 1;
 }
 
-// Groups per wave: enough lanes per group to cover N in one pass, at most 4
-// groups (16 lanes) and at least 1 (64 lanes, several passes for wide N).
+
+// Groups per wave: enough lanes per group to cover N in one pass, at most 8
+// groups (8 lanes of 16 bytes) and at least 1 (64 lanes, several passes for
+// wide N).
 int pick_groups(int N, int vec, int want) {
-    if (want == 1 || want == 2 || want == 4) return want;
+    if (want == 1 || want == 2 || want == 4 || (want == 8 && vec == 4)) return want;
     const int lanes = (N + vec - 1) / vec;
+    if (lanes <= 8 && vec == 4) return 8;
     if (lanes <= 16) return 4;
     if (lanes <= 32) return 2;
     return 1;
@@ -566,6 +569,9 @@ hipError_t dispatch_shape(int waves, int unroll, bool sbuf, const RowblockArgs& 
 template <int VEC>
 hipError_t dispatch_groups(int groups, int waves, int unroll, bool sbuf, const RowblockArgs& args,
                            int grid, hipStream_t stream) {
+    if constexpr (VEC == 4) {
+        if (groups == 8) return dispatch_shape<VEC, 8>(waves, unroll, sbuf, args, grid, stream);
+    }
     if (groups == 4) return dispatch_shape<VEC, 4>(waves, unroll, sbuf, args, grid, stream);
     if (groups == 2) return dispatch_shape<VEC, 2>(waves, unroll, sbuf, args, grid, stream);
     return dispatch_shape<VEC, 1>(waves, unroll, sbuf, args, grid, stream);

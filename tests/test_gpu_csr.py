@@ -54,7 +54,7 @@ def _edge_cases(S):
     v = rng.uniform(-1, 1, len(keep))
     cases["ragged"] = (_coo_csr(S, M, K, np.array(r)[keep], np.array(c)[keep], v),
                        rng.uniform(-1, 1, (K, 128)))
-    for N in (1, 3, 17, 64, 96, 130, 256, 257, 512):
+    for N in (1, 3, 17, 20, 32, 64, 96, 130, 256, 257, 512):
         A = S.generate_uniform_random_csr(200, 300, 0.05, N)
         cases[f"n{N}"] = (A, rng.uniform(-1, 1, (300, N)))
     # power-law rows at a small size: 2 .. 2000 entries per row
@@ -133,13 +133,14 @@ def test_engine_deterministic(S, torch, config_refs):
 
 
 @pytest.mark.parametrize("vec", [1, 2, 4])
-@pytest.mark.parametrize("groups", [1, 2, 4])
+@pytest.mark.parametrize("groups", [1, 2, 4, 8])
 @pytest.mark.parametrize("waves,unroll,gl", [(2, 8, 0), (4, 4, 0), (8, 8, 0), (8, 4, 1)])
 def test_engine_variants(S, torch, edge_cases, config_refs, vec, groups, waves, unroll, gl):
     # gl = 1: B through 64-bit address loads (the form used when B does not
     # fit a buffer resource) instead of structured-buffer loads
     opts = S.EngineOptsT(vec, waves, unroll, 0, groups, 0, gl)
-    for name in ("ragged", "power_law_small", "n3", "n17", "n96", "n257", "n512", "empty_nnz"):
+    for name in ("ragged", "power_law_small", "n3", "n17", "n20", "n32", "n96", "n257", "n512",
+                 "empty_nnz"):
         A, B, C64, absC = edge_cases[name]
         say(f"csr engine vec={vec} groups={groups} waves={waves} unroll={unroll} gl={gl} case={name}")
         dA = S.DeviceCSR(A)

@@ -27,13 +27,17 @@ struct HybridPlan {
 };
 
 // Fill-in at or below which the MFMA path wins on MI355X.  Timing both back
-// ends (spmm_tiled_v3 and spmm_wmma kernels, warm) on uniform-random inputs
-// of 4096^2 .. 16384^2 at N = 128 and 256: the MFMA path is faster at fill
-// 10 (1.3 - 2.4x) and at fill 20 (0.8 - 1.6x), the CSR engine at fill 33 and
-// above (1.0 - 1.7x); block-structured inputs cross between fill 25 and 45.
-// The reference's 2.0 was the crossover of a T4, whose tensor cores are far
-// less ahead of its CUDA cores.
-constexpr float kHybridDefaultThreshold = 24.0f;
+// ends (spmm_tiled_v3 and spmm_wmma kernels, warm) on 61 inputs -- uniform
+// random 4096^2 .. 16384^2 at fill 10 .. 50, random and banded partially
+// filled blocks at fill 10 .. 45, the five BASELINE configs -- at N = 128 and
+// 256: a cut-off anywhere in 16 .. 19 loses least to the faster back end
+// (6.4% on average; 24 loses 6.8% and 11x the time, mostly on large uniform
+// inputs at fill 20, where the CSR engine is 1.2 - 1.5x faster).  The
+// remaining misses are small block-structured inputs at fill 20 - 45, where
+// both kernels sit within 1.5 us of their launch cost.  The reference's 2.0
+// was the crossover of a T4, whose tensor cores are far less ahead of its
+// CUDA cores.
+constexpr float kHybridDefaultThreshold = 18.0f;
 
 HybridPlan hybrid_choose(const CSR& h_A, int N,
                          float fill_in_threshold = kHybridDefaultThreshold);

@@ -54,6 +54,9 @@ def _edge_cases(S):
     v = rng.uniform(-1, 1, len(keep))
     cases["ragged"] = (_coo_csr(S, M, K, np.array(r)[keep], np.array(c)[keep], v),
                        rng.uniform(-1, 1, (K, 128)))
+    # the same rows at N = 520: each wave's range spans several LDS windows
+    # (the 3000-entry row) and every window is walked in three column passes
+    cases["ragged_wide"] = (cases["ragged"][0], rng.uniform(-1, 1, (K, 520)))
     for N in (1, 3, 17, 20, 32, 64, 96, 130, 256, 257, 512):
         A = S.generate_uniform_random_csr(200, 300, 0.05, N)
         cases[f"n{N}"] = (A, rng.uniform(-1, 1, (300, N)))
@@ -139,8 +142,8 @@ def test_engine_variants(S, torch, edge_cases, config_refs, vec, groups, waves, 
     # gl = 1: B through 64-bit address loads (the form used when B does not
     # fit a buffer resource) instead of structured-buffer loads
     opts = S.EngineOptsT(vec, waves, unroll, 0, groups, 0, gl)
-    for name in ("ragged", "power_law_small", "n3", "n17", "n20", "n32", "n96", "n257", "n512",
-                 "empty_nnz"):
+    for name in ("ragged", "ragged_wide", "power_law_small", "n3", "n17", "n20", "n32", "n96",
+                 "n257", "n512", "empty_nnz"):
         A, B, C64, absC = edge_cases[name]
         say(f"csr engine vec={vec} groups={groups} waves={waves} unroll={unroll} gl={gl} case={name}")
         dA = S.DeviceCSR(A)
@@ -164,8 +167,8 @@ def test_engine_variants(S, torch, edge_cases, config_refs, vec, groups, waves, 
 @pytest.mark.parametrize("vec", [0, 1])
 def test_engine_column_slices(S, torch, edge_cases, config_refs, slices, vec):
     opts = S.EngineOptsT(vec, 8, 4, 0, 0, slices)
-    for name in ("ragged", "power_law_small", "n1", "n3", "n17", "n96", "n130", "n257", "n512",
-                 "empty_nnz", "identity"):
+    for name in ("ragged", "ragged_wide", "power_law_small", "n1", "n3", "n17", "n96", "n130",
+                 "n257", "n512", "empty_nnz", "identity"):
         A, B, C64, absC = edge_cases[name]
         say(f"csr engine slices={slices} vec={vec} case={name}")
         dA = S.DeviceCSR(A)
@@ -208,8 +211,8 @@ def _split_run(S, torch, A, B, parts):
 def test_split_engine(S, torch, edge_cases, config_refs, parts):
     # merge-path partition: equal nonzero ranges per workgroup, rows cut
     # between workgroups and completed by the carry fix-up
-    names = ("ragged", "power_law_small", "identity", "k_is_1", "n1", "n3", "n17", "n96",
-             "n130", "n257", "n512", "one_by_one")
+    names = ("ragged", "ragged_wide", "power_law_small", "identity", "k_is_1", "n1", "n3", "n17",
+             "n96", "n130", "n257", "n512", "one_by_one")
     for name in names:
         A, B, C64, absC = edge_cases[name]
         p = max(1, min(parts, A.nnz))

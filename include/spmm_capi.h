@@ -104,6 +104,8 @@ typedef struct spmm_bsr_opts_t {
     int xcd_order; /* wave kernel: 0, 1 XCD-grouped workgroup order; 2 dispatch order */
     int rows;      /* wave kernel: block-rows per wave sharing staged B tiles: 1, 2, 4 */
     int split;     /* wave kernel: 4 = the four waves of a workgroup split one block-row */
+    int addressing; /* wave kernel: 0 B rows / A blocks as buffer records where they fit
+                       (tiles >= 2, N % 8 == 0), 1 pointer arithmetic */
 } spmm_bsr_opts_t;
 
 const char* spmm_c_last_error(void);

@@ -21,6 +21,14 @@
 #include "engine.h"
 #include "spmm/utils.h"
 
+typedef unsigned spmm_u32x4 __attribute__((ext_vector_type(4)));
+
+// Structured buffer load (LLVM's AMDGPU intrinsic; index = record, offset =
+// byte offset inside the record).  The intrinsic name is fixed by LLVM.
+__device__ spmm_u32x4 sbuf_load_u32x4(__amdgpu_buffer_rsrc_t rsrc, int index, int offset,
+                                      int soffset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
+
 namespace spmm {
 namespace engine {
 
@@ -29,6 +37,7 @@ namespace {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float    f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // fp32 -> fp16 (round to nearest even), 8 elements per lane on the aligned body.
 __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict__ src,
@@ -77,6 +86,7 @@ struct BsrArgs {
     int             tiles_n;    // wave kernel: column tiles (grid is 1-D)
     int             wg_total;   // wave kernel: workgroups launched
     int             xcd_order;  // wave kernel: 1 = XCD-grouped workgroup order
+    int             num_blocks;
 };
 
 // Workgroup -> (block-row group, column tile) for the 1-D wave-kernel grid.
@@ -225,6 +235,148 @@ __global__ __launch_bounds__(256) void bsr_wave_kernel(BsrArgs a) {
     for (int c0 = bs; c0 < be; c0 += 64) {  // 64 blocks per column-index chunk
         const int cnt = min(64, be - c0);
         const int np  = (cnt + 1) >> 1;     // pairs in this chunk
+        const int ci  = lane < cnt ? a.col_idx[c0 + lane] : 0;
+        PairRegs ring[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) load_pair(c0, 2 * min(d, np - 1), cnt, ci, ring[d]);
+        int i0 = 0;
+        for (; i0 + 2 * D <= np; i0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                multiply(ring[d]);
+                load_pair(c0, 2 * (i0 + d + D), cnt, ci, ring[d]);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (i0 + d < np) {
+                multiply(ring[d]);
+                if (i0 + d + D < np) load_pair(c0, 2 * (i0 + d + D), cnt, ci, ring[d]);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (i0 + D + d < np) multiply(ring[d]);
+        }
+    }
+
+    // D layout: lane holds rows 4*g + i, column t of each 16-column tile.
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int col = n0 + 16 * j + t;
+        if (col >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = br * 16 + 4 * g + i;
+            if (row < a.M) store_c(a.C + static_cast<size_t>(row) * a.N + col, acc[j][i]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Record-addressed wave kernel (the default where it applies): the wave
+// kernel's work split and ring, with B and the A blocks read as structured
+// buffers -- one record per B row (N fp16) and one per 16x16 block.  The row
+// or block number is the load's index operand, and the buffer range check
+// returns zeros for an index past the end: rows >= K of a partial last
+// block-column, and index -1 for the absent second block of an odd tail.  So
+// a pair needs one index add per 16-byte chunk instead of 64-bit address
+// arithmetic and per-lane zero selects (measured on MI355X: ~30 -> ~6 vector
+// instructions per pair; c3 4.6 -> 4.3 us, c4 7.8 -> 7.1 us, identical
+// results).  Needs J >= 2 (each staged 16-byte chunk then belongs to one
+// block), N % 8 == 0 with 16-byte aligned B, N * 2 <= 16383 (record stride
+// field), and B and A each within 2 GiB.
+// ---------------------------------------------------------------------------
+// Third dword of a gfx9 buffer resource: 32-bit data format, no swizzle.
+constexpr int kBufWord3 = 0x00020000;
+
+template <int J, int D>
+__global__ __launch_bounds__(256) void bsr_record_kernel(BsrArgs a) {
+    constexpr int NT  = 16 * J;          // columns per wave
+    constexpr int S   = NT + 16;         // LDS row stride in fp16 (S/2 = 8 mod 32 banks)
+    constexpr int CH  = NT / 8;          // 16-byte chunks per staged row
+    constexpr int CPL = 32 * CH / 64;    // chunks per lane
+    static_assert(J >= 2, "each chunk must belong to one block of the pair");
+    __shared__ __attribute__((aligned(16))) _Float16 s_b[4][32 * S];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g    = lane >> 4;
+    const int t    = lane & 15;
+    int bx, by;
+    wave_tile_of(a, bx, by);
+    const int br   = bx * 4 + wave;
+    const int n0   = by * NT;
+    if (br >= a.block_rows) return;  // waves are independent: no barrier anywhere
+    _Float16* tile = s_b[wave];
+
+    const __amdgpu_buffer_rsrc_t rec_b = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(a.B), static_cast<short>(a.N * 2), a.K, kBufWord3);
+    const __amdgpu_buffer_rsrc_t rec_a = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(a.vals), static_cast<short>(512), a.num_blocks, kBufWord3);
+
+    // Lane constants: chunk c is staged row srow[c] (block srow >= 16 of the
+    // pair), columns n .. n+7 at byte offset nbyte[c] of its B row.  Columns
+    // past N read a valid chunk of the row instead; their products land in
+    // output columns >= N, which are never stored.
+    int srow[CPL], nbyte[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        const int idx = lane + c * 64;
+        srow[c] = idx / CH;
+        const int n = n0 + (idx % CH) * 8;
+        nbyte[c] = (n < a.N ? n : 0) * 2;
+    }
+    // A operand: row t of block (first, g < 2) or (second, g >= 2), columns 8*(g&1) .. +7
+    const int a_off = t * 32 + 16 * (g & 1);
+    const int a_hi  = g >> 1;
+
+    const int bs = a.row_ptr[br];
+    const int be = a.row_ptr[br + 1];
+
+    f32x4 acc[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) acc[j] = f32x4(0.0f);
+
+    struct PairRegs {
+        u32x4 b[CPL];
+        u32x4 af;
+    };
+    // Pair = blocks base+p and base+p+1 of the row (p and p+1 inside the
+    // column-index chunk ci that starts at block base).
+    auto load_pair = [&](int base, int p, int cnt, int ci, PairRegs& r) {
+        const bool two = p + 1 < cnt;
+        const int bc0 = __builtin_amdgcn_readlane(ci, p);
+        const int bc1 = two ? __builtin_amdgcn_readlane(ci, p + 1) : -1;  // rows -16..-1: zeros
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int sr = srow[c];
+            r.b[c] = sbuf_load_u32x4(rec_b, (sr < 16 ? bc0 : bc1) * 16 + (sr & 15), nbyte[c], 0, 0);
+        }
+        r.af = sbuf_load_u32x4(rec_a, (two || a_hi == 0) ? base + p + a_hi : -1, a_off, 0, 0);
+    };
+    auto multiply = [&](const PairRegs& r) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            const int idx = lane + c * 64;
+            *reinterpret_cast<u32x4*>(&tile[(idx / CH) * S + (idx % CH) * 8]) = r.b[c];
+        }
+        const f16x8 af = __builtin_bit_cast(f16x8, r.af);
+        const _Float16* rowp = &tile[(8 * g + (t >> 2)) * S + 4 * (t & 3)];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const s16x4 lo = lds_read_tr16(rowp + 16 * j);
+            const s16x4 hi = lds_read_tr16(rowp + 4 * S + 16 * j);
+            const s16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(f16x8, both),
+                                                             acc[j], 0, 0, 0);
+        }
+    };
+
+    // D pairs in flight, as in the wave kernel.
+    for (int c0 = bs; c0 < be; c0 += 64) {
+        const int cnt = min(64, be - c0);
+        const int np  = (cnt + 1) >> 1;
         const int ci  = lane < cnt ? a.col_idx[c0 + lane] : 0;
         PairRegs ring[D];
 #pragma unroll
@@ -832,13 +984,27 @@ Error from_hip(hipError_t e, const char* what) {
     return fail(kHipError, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+// B rows and A blocks fit structured-buffer records: the record stride field
+// holds at most 16383 bytes and each buffer must stay within 2 GiB.
+bool records_fit(const BsrArgs& a) {
+    return a.b_vec_ok && static_cast<long long>(a.N) * 2 <= 16383 &&
+           static_cast<long long>(a.K) * a.N * 2 <= 0x7fffffffLL &&
+           static_cast<long long>(a.num_blocks) * 512 <= 0x7fffffffLL;
+}
+
 template <int J, int D>
-hipError_t run_wave(BsrArgs args, hipStream_t stream) {
+hipError_t run_wave(BsrArgs args, hipStream_t stream, bool pointer_addressing) {
     args.tiles_n = ceil_div(args.N, 16 * J);
     const long total = static_cast<long>(ceil_div(args.block_rows, 4)) * args.tiles_n;
     if (total > 0x7fffffffL) return hipErrorInvalidConfiguration;
     args.wg_total = static_cast<int>(total);
     dim3 grid(args.wg_total);
+    if constexpr (J >= 2) {
+        if (!pointer_addressing && records_fit(args)) {
+            hipLaunchKernelGGL((bsr_record_kernel<J, D>), grid, dim3(256), 0, stream, args);
+            return hipGetLastError();
+        }
+    }
     if (args.b_vec_ok) {
         hipLaunchKernelGGL((bsr_wave_kernel<J, D, true>), grid, dim3(256), 0, stream, args);
     } else {
@@ -848,9 +1014,11 @@ hipError_t run_wave(BsrArgs args, hipStream_t stream) {
 }
 
 template <int J>
-hipError_t dispatch_wave(int depth, const BsrArgs& args, hipStream_t stream) {
-    return depth == 1 ? run_wave<J, 1>(args, stream)
-                      : (depth == 2 ? run_wave<J, 2>(args, stream) : run_wave<J, 4>(args, stream));
+hipError_t dispatch_wave(int depth, bool pointer_addressing, const BsrArgs& args,
+                         hipStream_t stream) {
+    return depth == 1 ? run_wave<J, 1>(args, stream, pointer_addressing)
+                      : (depth == 2 ? run_wave<J, 2>(args, stream, pointer_addressing)
+                                    : run_wave<J, 4>(args, stream, pointer_addressing));
 }
 
 template <int R, int J, int D>
@@ -967,7 +1135,8 @@ Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t strea
                  A.block_cols,
                  0,
                  0,
-                 0};
+                 0,
+                 A.num_blocks};
     const BsrOpts o = opts ? *opts : BsrOpts{};
     args.xcd_order = o.xcd_order == 2 ? 0 : 1;
     hipError_t e;
@@ -989,8 +1158,10 @@ Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t strea
                             : dispatch_multirow<4>(j, dm, args, stream);
             return from_hip(e, "spmm_wmma launch");
         }
-        e = j == 1 ? dispatch_wave<1>(d, args, stream)
-                   : (j == 2 ? dispatch_wave<2>(d, args, stream) : dispatch_wave<4>(d, args, stream));
+        const bool ptr = o.addressing == 1;
+        e = j == 1 ? dispatch_wave<1>(d, ptr, args, stream)
+                   : (j == 2 ? dispatch_wave<2>(d, ptr, args, stream)
+                             : dispatch_wave<4>(d, ptr, args, stream));
         return from_hip(e, "spmm_wmma launch");
     }
     int j = o.tiles;

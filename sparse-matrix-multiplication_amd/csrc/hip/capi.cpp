@@ -625,6 +625,7 @@ int spmm_c_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B16, float* d_C,
         o.xcd_order = opts->xcd_order;
         o.rows      = opts->rows;
         o.split     = opts->split;
+        o.addressing = opts->addressing;
     }
     return from_engine(spmm::engine::launch_bsr(to_cpp(*d_bsr),
                                                 reinterpret_cast<const half*>(d_B16), d_C, N,

@@ -69,6 +69,7 @@ struct BsrOpts {
     int xcd_order = 0;  // wave kernel: 0, 1 XCD-grouped workgroup order; 2 dispatch order
     int rows      = 0;  // wave kernel: block-rows per wave sharing staged B tiles, 1, 2 or 4
     int split     = 0;  // wave kernel: 4 = the four waves of a workgroup split one block-row
+    int addressing = 0; // wave kernel: 0 buffer records where they fit, 1 pointer arithmetic
 };
 
 Error launch_bsr(const BSR& d_A, const half* d_B, float* d_C, int N, hipStream_t stream,

@@ -97,20 +97,26 @@ def test_wmma_cases(S, O, torch, name):
                                                        (8, 1, 0), (8, 4, 0), (8, 8, 0),
                                                        (0, 1, 1), (0, 2, 1), (0, 4, 1)])
 @pytest.mark.parametrize("depth", [1, 2, 4])
-def test_wmma_variants(S, O, torch, row_group, tiles, per_wave, depth):
+@pytest.mark.parametrize("addressing", [0, 1])
+def test_wmma_variants(S, O, torch, row_group, tiles, per_wave, depth, addressing):
+    # addressing 0: B rows and A blocks as buffer records (tiles >= 2, N % 8 == 0),
+    # 1: the pointer-arithmetic wave kernel
     if depth != 2 and (row_group != 0 or per_wave == 0):
         pytest.skip("depth applies to the wave kernel only")
+    if addressing == 1 and per_wave == 0:
+        pytest.skip("addressing applies to the wave kernel only")
     cases = _cases(S)
     for name in ("single_block", "odd_pair_count", "ragged_dims", "n_not_16", "n_1",
                  "empty_block_rows", "empty", "wide_n", "block_diag_small"):
         A, B = cases[name]
         hb, B16, C32, C64, absC = _refs(S, O, A, B)
         say(f"wmma opts row_group={row_group} tiles={tiles} per_wave={per_wave} depth={depth} "
-            f"case={name}")
+            f"addressing={addressing} case={name}")
         dA = S.DeviceBSR(hb)
         dB = torch.from_numpy(B16.view(np.int16)).cuda()
         dC = torch.full((hb.num_rows, B16.shape[1]), float("nan"), device="cuda")
-        S.spmm_wmma_opts(dA, dB, S.BsrOptsT(row_group, tiles, per_wave, depth), dC)
+        S.spmm_wmma_opts(dA, dB, S.BsrOptsT(row_group, tiles, per_wave, depth, 0, 0, 0,
+                                            addressing), dC)
         torch.cuda.synchronize()
         C = dC.cpu().numpy()
         check_bsr(C, C32, absC)
@@ -149,11 +155,13 @@ def test_wmma_chunk_boundaries(S, O, torch):
     assert list(np.diff(hb.row_ptr)) == [63, 64, 65, 128, 129, 1, 0, 2]
     for tiles in (1, 2, 4):
         for depth in (1, 2, 4):
-            say(f"wmma chunk boundaries tiles={tiles} depth={depth}")
-            C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
-                                 S.BsrOptsT(0, tiles, 1, depth)).cpu().numpy()
-            check_bsr(C, C32, absC)
-            check_csr(C, C64, absC, tol=1e-5)
+            for addressing in (0, 1):
+                say(f"wmma chunk boundaries tiles={tiles} depth={depth} addressing={addressing}")
+                C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
+                                     S.BsrOptsT(0, tiles, 1, depth, 0, 0, 0,
+                                                addressing)).cpu().numpy()
+                check_bsr(C, C32, absC)
+                check_csr(C, C64, absC, tol=1e-5)
 
 
 @pytest.mark.parametrize("rows", [2, 4])

@@ -57,7 +57,7 @@ def _edge_cases(S):
     # the same rows at N = 520: each wave's range spans several LDS windows
     # (the 3000-entry row) and every window is walked in three column passes
     cases["ragged_wide"] = (cases["ragged"][0], rng.uniform(-1, 1, (K, 520)))
-    for N in (1, 3, 17, 20, 32, 64, 96, 130, 256, 257, 512):
+    for N in (1, 3, 17, 20, 32, 64, 96, 130, 256, 257, 512, 4100):
         A = S.generate_uniform_random_csr(200, 300, 0.05, N)
         cases[f"n{N}"] = (A, rng.uniform(-1, 1, (300, N)))
     # power-law rows at a small size: 2 .. 2000 entries per row
@@ -143,7 +143,7 @@ def test_engine_variants(S, torch, edge_cases, config_refs, vec, groups, waves, 
     # fit a buffer resource) instead of structured-buffer loads
     opts = S.EngineOptsT(vec, waves, unroll, 0, groups, 0, gl)
     for name in ("ragged", "ragged_wide", "power_law_small", "n3", "n17", "n20", "n32", "n96",
-                 "n257", "n512", "empty_nnz"):
+                 "n257", "n512", "n4100", "empty_nnz"):
         A, B, C64, absC = edge_cases[name]
         say(f"csr engine vec={vec} groups={groups} waves={waves} unroll={unroll} gl={gl} case={name}")
         dA = S.DeviceCSR(A)

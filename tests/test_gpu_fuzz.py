@@ -1,0 +1,120 @@
+"""Seeded random parity sweep on cuda:0: random shapes, densities, row-length
+skew and engine options for the CSR engine (row partition and merge-path), and
+random shapes and kernel options for the MFMA BSR kernel, each checked against
+the CPU oracle with the same bars as the other GPU tests (fp32 CSR within
+1e-5 of the fp64 loop; fp16 BSR within 1e-2 of fp32 accumulation and within
+1e-5 of the exact product of the fp16 operands)."""
+import numpy as np
+import pytest
+
+from gpu_util import check_bsr, check_csr
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    assert t.cuda.is_available(), "GPU tests need cuda:0"
+    return t
+
+
+def _skewed_csr(S, rng, M, K):
+    """Rows of very different lengths (empty rows included), unique columns per row."""
+    rows, cols = [], []
+    for r in range(M):
+        u = rng.random()
+        if u < 0.2:
+            n = 0
+        elif u < 0.9:
+            n = int(rng.integers(1, max(2, min(K, 40))))
+        else:
+            n = int(rng.integers(1, K + 1))  # up to a full row
+        if n:
+            rows.append(np.full(n, r))
+            cols.append(rng.choice(K, n, replace=False))
+    if not rows:
+        return S.csr_from_coo_host(M, K, [], [], [])
+    r = np.concatenate(rows)
+    c = np.concatenate(cols)
+    return S.csr_from_coo_host(M, K, r, c, rng.uniform(-1, 1, r.size).astype(np.float32))
+
+
+def _random_csr(S, rng, M, K):
+    kind = int(rng.integers(0, 3))
+    if kind == 0:
+        return S.generate_uniform_random_csr(M, K, float(rng.uniform(0.0, 0.15)),
+                                             int(rng.integers(1, 10000)))
+    if kind == 1:
+        mean = float(rng.uniform(1.0, max(1.5, min(K, 60))))
+        return S.generate_power_law_csr(M, K, mean, 1.5, K, int(rng.integers(1, 10000)))
+    return _skewed_csr(S, rng, M, K)
+
+
+def _shape(rng):
+    M = int(rng.integers(1, 600))
+    K = int(rng.integers(1, 800))
+    N = int(rng.choice([1, 2, 3, 4, 8, 16, 20, 31, 32, 48, 64, 100, 128, 130, 192, 256, 300]))
+    return M, K, N
+
+
+@pytest.mark.parametrize("chunk", range(4))
+def test_csr_engine_random(S, O, torch, chunk):
+    rng = np.random.default_rng(1000 + chunk)
+    for case in range(30):
+        M, K, N = _shape(rng)
+        A = _random_csr(S, rng, M, K)
+        B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+        opts = S.EngineOptsT(int(rng.choice([0, 1, 2, 4])), int(rng.choice([0, 2, 4, 8])),
+                             int(rng.choice([0, 4, 8])),
+                             int(rng.choice([0, 0, 1, 3, 16, 64])),
+                             int(rng.choice([0, 1, 2, 4, 8])), int(rng.choice([0, 1, 2, 4, 8])),
+                             int(rng.choice([0, 0, 1])))
+        say(f"fuzz csr chunk={chunk} case={case} M={M} K={K} N={N} nnz={A.nnz} "
+            f"opts=({opts.vec},{opts.waves},{opts.unroll},{opts.rows_per_block},{opts.groups},"
+            f"{opts.slices},{opts.global_loads})")
+        C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)
+        dA = S.DeviceCSR(A)
+        dB = torch.from_numpy(B).cuda()
+        dC = torch.full((M, N), float("nan"), device="cuda")
+        S.spmm_tiled_v3_opts(dA, dB, opts, dC)
+        torch.cuda.synchronize()
+        check_csr(dC.cpu().numpy(), C64, absC)
+        if A.nnz > 0 and case % 3 == 0:
+            parts = int(rng.integers(1, A.nnz + 1))
+            say(f"fuzz csr split chunk={chunk} case={case} parts={parts}")
+            rows = torch.from_numpy(S.nnz_split_rows(A, parts)).cuda()
+            dC.fill_(float("nan"))
+            S.spmm_tiled_v3_split(dA, rows, dB, dC)
+            torch.cuda.synchronize()
+            check_csr(dC.cpu().numpy(), C64, absC)
+
+
+@pytest.mark.parametrize("chunk", range(3))
+def test_mfma_random(S, O, torch, chunk):
+    rng = np.random.default_rng(2000 + chunk)
+    for case in range(25):
+        M, K, N = _shape(rng)
+        A = _random_csr(S, rng, M, K)
+        A.values = S.round_to_fp16(A.values)
+        B = S.round_to_fp16(rng.uniform(-1, 1, (K, N)).astype(np.float32))
+        hb = S.bsr_from_csr_host(A)
+        B16 = O.f32_to_f16(B)
+        C32 = O.bsr_spmm_f32(M, K, hb.row_ptr, hb.col_idx, hb.values, B16, threads=8)
+        C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B16.view(np.float16)
+                                   .astype(np.float32), threads=8)
+        opts = S.BsrOptsT(0, int(rng.choice([0, 1, 2, 4])), 1, int(rng.choice([0, 1, 2, 4])),
+                          int(rng.choice([0, 1, 2])), 0, 0, int(rng.choice([0, 1])))
+        say(f"fuzz mfma chunk={chunk} case={case} M={M} K={K} N={N} blocks={hb.num_blocks} "
+            f"opts=(tiles {opts.tiles}, depth {opts.depth}, order {opts.xcd_order}, "
+            f"addressing {opts.addressing})")
+        dC = torch.full((M, N), float("nan"), device="cuda")
+        S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(), opts, dC)
+        torch.cuda.synchronize()
+        C = dC.cpu().numpy()
+        check_bsr(C, C32, absC)
+        check_csr(C, C64, absC, tol=1e-5)

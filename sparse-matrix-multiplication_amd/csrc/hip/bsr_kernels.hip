@@ -28,6 +28,12 @@ typedef unsigned spmm_u32x4 __attribute__((ext_vector_type(4)));
 __device__ spmm_u32x4 sbuf_load_u32x4(__amdgpu_buffer_rsrc_t rsrc, int index, int offset,
                                       int soffset, int aux)
     __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
+// Structured buffer load straight into LDS: every lane's `size` bytes land at
+// the LDS address p + 16 * lane (gfx950 LDS DMA), nothing passes through VGPRs.
+typedef __attribute__((address_space(3))) void* spmm_lds_ptr;
+__device__ void sbuf_load_lds(__amdgpu_buffer_rsrc_t rsrc, spmm_lds_ptr p, int size, int index,
+                              int offset, int soffset, int imm_offset, int aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.lds");
 
 namespace spmm {
 namespace engine {
@@ -281,23 +287,46 @@ __global__ __launch_bounds__(256) void bsr_wave_kernel(BsrArgs a) {
 // returns zeros for an index past the end: rows >= K of a partial last
 // block-column, and index -1 for the absent second block of an odd tail.  So
 // a pair needs one index add per 16-byte chunk instead of 64-bit address
-// arithmetic and per-lane zero selects (measured on MI355X: ~30 -> ~6 vector
-// instructions per pair; c3 4.6 -> 4.3 us, c4 7.8 -> 7.1 us, identical
-// results).  Needs J >= 2 (each staged 16-byte chunk then belongs to one
-// block), N % 8 == 0 with 16-byte aligned B, N * 2 <= 16383 (record stride
-// field), and B and A each within 2 GiB.
+// arithmetic and per-lane zero selects (~30 -> ~6 vector instructions per
+// pair).  The B rows of a pair go straight into the wave's LDS slot with
+// buffer-to-LDS loads (no VGPR staging, no ds_write), one slot per pair in
+// flight, each slot its own LDS object.  Measured on MI355X against the same
+// kernel staging through VGPRs and ds_write (both at their default tiles):
+// banded 8192^2 N=128 4.3 -> 4.1 us, block-diagonal 8192^2 N=256 6.4 -> 6.1
+// us, identical results.  Needs N % 8 == 0 with 16-byte aligned B, N * 2 <= 16383 (record
+// stride field), and B and A within 2 GiB each.
 // ---------------------------------------------------------------------------
+__device__ u32x4 sbuf_load_u32x4_dev(__amdgpu_buffer_rsrc_t rsrc, int index, int offset) {
+    return sbuf_load_u32x4(rsrc, index, offset, 0, 0);
+}
+
 // Third dword of a gfx9 buffer resource: 32-bit data format, no swizzle.
 constexpr int kBufWord3 = 0x00020000;
 
+// s_waitcnt constraining only the vector-memory count (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).
+template <int VM>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(VM >= 0 && VM < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt((VM & 0xF) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 template <int J, int D>
 __global__ __launch_bounds__(256) void bsr_record_kernel(BsrArgs a) {
-    constexpr int NT  = 16 * J;          // columns per wave
-    constexpr int S   = NT + 16;         // LDS row stride in fp16 (S/2 = 8 mod 32 banks)
-    constexpr int CH  = NT / 8;          // 16-byte chunks per staged row
-    constexpr int CPL = 32 * CH / 64;    // chunks per lane
-    static_assert(J >= 2, "each chunk must belong to one block of the pair");
-    __shared__ __attribute__((aligned(16))) _Float16 s_b[4][32 * S];
+    constexpr int NT   = 16 * J;       // columns per wave
+    constexpr int CH   = NT / 8;       // 16-byte chunks per staged row
+    constexpr int CPL  = 32 * CH / 64; // chunks per lane (one load instruction each)
+    constexpr int TILE = 32 * NT;      // fp16 per slot: the pair's 32 B rows, row-major
+    constexpr int PER  = CPL + 1;      // vector-memory instructions per pair
+    static_assert(D == 2 || D == 4, "ring depth 2 or 4");
+    // One LDS object per ring slot: the compiler then knows which slot a
+    // buffer-to-LDS load writes and which slot a read waits for.
+    __shared__ __attribute__((aligned(16))) _Float16 s_b0[4][TILE];
+    __shared__ __attribute__((aligned(16))) _Float16 s_b1[4][TILE];
+    __shared__ __attribute__((aligned(16))) _Float16 s_b2[4][D == 4 ? TILE : 8];
+    __shared__ __attribute__((aligned(16))) _Float16 s_b3[4][D == 4 ? TILE : 8];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -308,17 +337,20 @@ __global__ __launch_bounds__(256) void bsr_record_kernel(BsrArgs a) {
     const int br   = bx * 4 + wave;
     const int n0   = by * NT;
     if (br >= a.block_rows) return;  // waves are independent: no barrier anywhere
-    _Float16* tile = s_b[wave];
+    auto slot = [&](int d) -> _Float16* {
+        return (d == 0 ? s_b0[0] : d == 1 ? s_b1[0] : d == 2 ? s_b2[0] : s_b3[0]) + wave * TILE;
+    };
 
     const __amdgpu_buffer_rsrc_t rec_b = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<_Float16*>(a.B), static_cast<short>(a.N * 2), a.K, kBufWord3);
     const __amdgpu_buffer_rsrc_t rec_a = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<_Float16*>(a.vals), static_cast<short>(512), a.num_blocks, kBufWord3);
 
-    // Lane constants: chunk c is staged row srow[c] (block srow >= 16 of the
-    // pair), columns n .. n+7 at byte offset nbyte[c] of its B row.  Columns
-    // past N read a valid chunk of the row instead; their products land in
-    // output columns >= N, which are never stored.
+    // Lane constants: load instruction c moves 16-byte chunk idx = lane + 64c,
+    // staged row srow (block srow >= 16 of the pair), columns n .. n+7 at byte
+    // offset nbyte of its B row, to slot offset 8 * idx fp16 (row-major).
+    // Columns past N read a valid chunk of the row instead; their products
+    // land in output columns >= N, which are never stored.
     int srow[CPL], nbyte[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -338,67 +370,69 @@ __global__ __launch_bounds__(256) void bsr_record_kernel(BsrArgs a) {
 #pragma unroll
     for (int j = 0; j < J; ++j) acc[j] = f32x4(0.0f);
 
-    struct PairRegs {
-        u32x4 b[CPL];
-        u32x4 af;
-    };
+    u32x4 af[D];
     // Pair = blocks base+p and base+p+1 of the row (p and p+1 inside the
-    // column-index chunk ci that starts at block base).
-    auto load_pair = [&](int base, int p, int cnt, int ci, PairRegs& r) {
+    // column-index chunk ci that starts at block base), into ring slot d.
+    auto load_pair = [&](int d, int base, int p, int cnt, int ci) {
         const bool two = p + 1 < cnt;
         const int bc0 = __builtin_amdgcn_readlane(ci, p);
         const int bc1 = two ? __builtin_amdgcn_readlane(ci, p + 1) : -1;  // rows -16..-1: zeros
+        _Float16* dst = slot(d);
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             const int sr = srow[c];
-            r.b[c] = sbuf_load_u32x4(rec_b, (sr < 16 ? bc0 : bc1) * 16 + (sr & 15), nbyte[c], 0, 0);
+            sbuf_load_lds(rec_b, (spmm_lds_ptr)(dst + c * 512), 16,
+                          (sr < 16 ? bc0 : bc1) * 16 + (sr & 15), nbyte[c], 0, 0, 0);
         }
-        r.af = sbuf_load_u32x4(rec_a, (two || a_hi == 0) ? base + p + a_hi : -1, a_off, 0, 0);
+        af[d] = sbuf_load_u32x4_dev(rec_a, (two || a_hi == 0) ? base + p + a_hi : -1, a_off);
     };
-    auto multiply = [&](const PairRegs& r) {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            const int idx = lane + c * 64;
-            *reinterpret_cast<u32x4*>(&tile[(idx / CH) * S + (idx % CH) * 8]) = r.b[c];
-        }
-        const f16x8 af = __builtin_bit_cast(f16x8, r.af);
-        const _Float16* rowp = &tile[(8 * g + (t >> 2)) * S + 4 * (t & 3)];
+    auto multiply = [&](int d) {
+        const f16x8 afv = __builtin_bit_cast(f16x8, af[d]);
+        const _Float16* rowp = slot(d) + (8 * g + (t >> 2)) * NT + 4 * (t & 3);
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const s16x4 lo = lds_read_tr16(rowp + 16 * j);
-            const s16x4 hi = lds_read_tr16(rowp + 4 * S + 16 * j);
+            const s16x4 hi = lds_read_tr16(rowp + 4 * NT + 16 * j);
             const s16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(f16x8, both),
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afv, __builtin_bit_cast(f16x8, both),
                                                              acc[j], 0, 0, 0);
         }
     };
 
-    // D pairs in flight, as in the wave kernel.
-    for (int c0 = bs; c0 < be; c0 += 64) {
+    // D pairs in flight.  Vector-memory instructions retire in issue order,
+    // so before slot d is read, waiting until at most (D-1) pairs' loads are
+    // outstanding guarantees slot d's are done.  A slot is refilled only after
+    // the MFMAs that consumed its reads, so its reads are complete by then.
+    // The drain (fewer loads after each slot) waits for everything.
+    for (int c0 = bs; c0 < be; c0 += 64) {  // 64 blocks per column-index chunk
         const int cnt = min(64, be - c0);
         const int np  = (cnt + 1) >> 1;
         const int ci  = lane < cnt ? a.col_idx[c0 + lane] : 0;
-        PairRegs ring[D];
 #pragma unroll
-        for (int d = 0; d < D; ++d) load_pair(c0, 2 * min(d, np - 1), cnt, ci, ring[d]);
+        for (int d = 0; d < D; ++d) load_pair(d, c0, 2 * min(d, np - 1), cnt, ci);
         int i0 = 0;
         for (; i0 + 2 * D <= np; i0 += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                multiply(ring[d]);
-                load_pair(c0, 2 * (i0 + d + D), cnt, ci, ring[d]);
+                wait_vmcnt<(D - 1) * PER>();
+                multiply(d);
+                load_pair(d, c0, 2 * (i0 + d + D), cnt, ci);
             }
         }
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             if (i0 + d < np) {
-                multiply(ring[d]);
-                if (i0 + d + D < np) load_pair(c0, 2 * (i0 + d + D), cnt, ci, ring[d]);
+                wait_vmcnt<0>();
+                multiply(d);
+                if (i0 + d + D < np) load_pair(d, c0, 2 * (i0 + d + D), cnt, ci);
             }
         }
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            if (i0 + D + d < np) multiply(ring[d]);
+            if (i0 + D + d < np) {
+                wait_vmcnt<0>();
+                multiply(d);
+            }
         }
     }
 
@@ -999,11 +1033,10 @@ hipError_t run_wave(BsrArgs args, hipStream_t stream, bool pointer_addressing) {
     if (total > 0x7fffffffL) return hipErrorInvalidConfiguration;
     args.wg_total = static_cast<int>(total);
     dim3 grid(args.wg_total);
-    if constexpr (J >= 2) {
-        if (!pointer_addressing && records_fit(args)) {
-            hipLaunchKernelGGL((bsr_record_kernel<J, D>), grid, dim3(256), 0, stream, args);
-            return hipGetLastError();
-        }
+    if (!pointer_addressing && records_fit(args)) {
+        hipLaunchKernelGGL((bsr_record_kernel<J, D == 1 ? 2 : D>), grid, dim3(256), 0, stream,
+                           args);
+        return hipGetLastError();
     }
     if (args.b_vec_ok) {
         hipLaunchKernelGGL((bsr_wave_kernel<J, D, true>), grid, dim3(256), 0, stream, args);
@@ -1146,7 +1179,12 @@ Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t strea
         // Default: the wave kernel with two 16-column tiles and two pairs in
         // flight, measured fastest on MI355X for both the banded (c3, N = 128)
         // and the block-diagonal (c4, N = 256) configs.
-        const int j = (o.tiles == 1 || o.tiles == 2 || o.tiles == 4) ? o.tiles : (N <= 16 ? 1 : 2);
+        // Default tiles: 4 (64 columns per wave) for N >= 256, else 2.  Measured
+        // on MI355X: block-diagonal N=256 6.9 -> 6.5 us going from 2 to 4 tiles,
+        // banded N=128 4.0 -> 4.4 us.
+        const int j = (o.tiles == 1 || o.tiles == 2 || o.tiles == 4)
+                          ? o.tiles
+                          : (N <= 16 ? 1 : (N >= 256 ? 4 : 2));
         const int d = (o.depth == 1 || o.depth == 2 || o.depth == 4) ? o.depth : 2;
         if (o.split == 4) {
             e = dispatch_splitk(j, d == 1 ? 1 : 2, args, stream);

@@ -314,19 +314,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 template <int J, int D>
-__global__ __launch_bounds__(256) void bsr_record_kernel(BsrArgs a) {
+__device__ __forceinline__ void bsr_record_body(const BsrArgs& a, _Float16* __restrict__ s0,
+                                                _Float16* __restrict__ s1,
+                                                _Float16* __restrict__ s2,
+                                                _Float16* __restrict__ s3) {
     constexpr int NT   = 16 * J;       // columns per wave
     constexpr int CH   = NT / 8;       // 16-byte chunks per staged row
     constexpr int CPL  = 32 * CH / 64; // chunks per lane (one load instruction each)
     constexpr int TILE = 32 * NT;      // fp16 per slot: the pair's 32 B rows, row-major
     constexpr int PER  = CPL + 1;      // vector-memory instructions per pair
-    static_assert(D == 2 || D == 4, "ring depth 2 or 4");
-    // One LDS object per ring slot: the compiler then knows which slot a
-    // buffer-to-LDS load writes and which slot a read waits for.
-    __shared__ __attribute__((aligned(16))) _Float16 s_b0[4][TILE];
-    __shared__ __attribute__((aligned(16))) _Float16 s_b1[4][TILE];
-    __shared__ __attribute__((aligned(16))) _Float16 s_b2[4][D == 4 ? TILE : 8];
-    __shared__ __attribute__((aligned(16))) _Float16 s_b3[4][D == 4 ? TILE : 8];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -338,7 +334,7 @@ __global__ __launch_bounds__(256) void bsr_record_kernel(BsrArgs a) {
     const int n0   = by * NT;
     if (br >= a.block_rows) return;  // waves are independent: no barrier anywhere
     auto slot = [&](int d) -> _Float16* {
-        return (d == 0 ? s_b0[0] : d == 1 ? s_b1[0] : d == 2 ? s_b2[0] : s_b3[0]) + wave * TILE;
+        return (d == 0 ? s0 : d == 1 ? s1 : d == 2 ? s2 : s3) + wave * TILE;
     };
 
     const __amdgpu_buffer_rsrc_t rec_b = __builtin_amdgcn_make_buffer_rsrc(
@@ -447,6 +443,21 @@ __global__ __launch_bounds__(256) void bsr_record_kernel(BsrArgs a) {
             if (row < a.M) store_c(a.C + static_cast<size_t>(row) * a.N + col, acc[j][i]);
         }
     }
+}
+
+// The ring slots are separate LDS objects passed as restrict pointers: after
+// inlining, every slot access carries its own alias scope, which lets the
+// compiler's wait-count pass tell a read of slot d from the buffer-to-LDS
+// writes still in flight into the other slots.
+template <int J, int D>
+__global__ __launch_bounds__(256) void bsr_record_kernel(BsrArgs a) {
+    constexpr int TILE = 32 * 16 * J;
+    static_assert(D == 2 || D == 4, "ring depth 2 or 4");
+    __shared__ __attribute__((aligned(16))) _Float16 s_b0[4 * TILE];
+    __shared__ __attribute__((aligned(16))) _Float16 s_b1[4 * TILE];
+    __shared__ __attribute__((aligned(16))) _Float16 s_b2[D == 4 ? 4 * TILE : 8];
+    __shared__ __attribute__((aligned(16))) _Float16 s_b3[D == 4 ? 4 * TILE : 8];
+    bsr_record_body<J, D>(a, s_b0, s_b1, s_b2, s_b3);
 }
 
 // ---------------------------------------------------------------------------
@@ -1176,16 +1187,27 @@ Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t strea
     const int nwords = (A.block_cols + 31) / 32;
     const bool use_groups = o.row_group != 0 && !o.per_wave && nwords <= kMaxUnionWords;
     if (!use_groups) {
-        // Default: the wave kernel with two 16-column tiles and two pairs in
-        // flight, measured fastest on MI355X for both the banded (c3, N = 128)
-        // and the block-diagonal (c4, N = 256) configs.
-        // Default tiles: 4 (64 columns per wave) for N >= 256, else 2.  Measured
-        // on MI355X: block-diagonal N=256 6.9 -> 6.5 us going from 2 to 4 tiles,
-        // banded N=128 4.0 -> 4.4 us.
-        const int j = (o.tiles == 1 || o.tiles == 2 || o.tiles == 4)
-                          ? o.tiles
-                          : (N <= 16 ? 1 : (N >= 256 ? 4 : 2));
-        const int d = (o.depth == 1 || o.depth == 2 || o.depth == 4) ? o.depth : 2;
+        // Defaults of the wave kernel, from a sweep of 92 MI355X runs (uniform,
+        // banded, block-diagonal and power-law, M = 4096 .. 16384, N = 64 ..
+        // 512).  Four 16-column tiles per wave halve the A-block re-reads of
+        // two tiles and win once the grid still has >= 1024 waves at four
+        // tiles, unless block-rows are short (< 12 blocks) and the grid is
+        // under 2048 waves: then the extra waves of two tiles hide more latency
+        // (e.g. uniform 8192^2 density 0.01 N=128: 67 -> 48 us; banded 8192^2
+        // half-bandwidth 64 N=128 stays at two tiles, 4.0 vs 4.1 us).  Four
+        // pairs in flight pay on long block-rows: >= 30 blocks at two tiles,
+        // >= 96 at four (uniform 4096^2 density 0.01 N=128: 26.4 -> 20.3 us).
+        // The pointer-arithmetic form keeps two tiles and two pairs: it has no
+        // buffer-to-LDS staging, and four tiles measured slower there.
+        const bool rec = o.addressing != 1 && records_fit(args);
+        const double bpr = A.block_rows > 0 ? static_cast<double>(A.num_blocks) / A.block_rows : 0.0;
+        const long waves4 = static_cast<long>(A.block_rows) * ((N + 63) / 64);
+        const int j_auto =
+            N <= 16 ? 1
+                    : ((rec && waves4 >= 1024 && (bpr >= 12.0 || waves4 >= 2048)) ? 4 : 2);
+        const int j = (o.tiles == 1 || o.tiles == 2 || o.tiles == 4) ? o.tiles : j_auto;
+        const int d_auto = (rec && bpr >= (j == 4 ? 96.0 : 30.0)) ? 4 : 2;
+        const int d = (o.depth == 1 || o.depth == 2 || o.depth == 4) ? o.depth : d_auto;
         if (o.split == 4) {
             e = dispatch_splitk(j, d == 1 ? 1 : 2, args, stream);
             return from_hip(e, "spmm_wmma launch");

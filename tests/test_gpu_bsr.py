@@ -297,6 +297,20 @@ def test_wmma_on_uniform_c1(S, O, torch):
     check_bsr(_run_wmma(S, torch, hb, B16), C32, absC)
 
 
+def test_wmma_default_four_tiles_four_pairs(S, O, torch):
+    # 1024 block-rows of ~127 blocks at N = 64: the default picks four column
+    # tiles per wave and four pairs in flight
+    A = S.generate_uniform_random_csr(16384, 2048, 0.02, 41)
+    A.values = S.round_to_fp16(A.values)
+    B = S.round_to_fp16(np.random.default_rng(42).uniform(-1, 1, (2048, 64)).astype(np.float32))
+    hb, B16, C32, C64, absC = _refs(S, O, A, B)
+    assert hb.num_blocks / hb.block_rows >= 96
+    say(f"wmma default 4x4 blocks={hb.num_blocks}")
+    C = _run_wmma(S, torch, hb, B16)
+    check_bsr(C, C32, absC)
+    check_csr(C, C64, absC, tol=1e-5)
+
+
 def test_float_to_half_bitwise(S, O, torch):
     rng = np.random.default_rng(17)
     x = np.concatenate([rng.standard_normal(100003).astype(np.float32) * s

@@ -30,14 +30,14 @@ struct HybridPlan {
 // ends (spmm_tiled_v3 and spmm_wmma kernels, warm) on 61 inputs -- uniform
 // random 4096^2 .. 16384^2 at fill 10 .. 50, random and banded partially
 // filled blocks at fill 10 .. 45, the five BASELINE configs -- at N = 128 and
-// 256: a cut-off anywhere in 16 .. 19 loses least to the faster back end
-// (6.4% on average; 24 loses 6.8% and 11x the time, mostly on large uniform
-// inputs at fill 20, where the CSR engine is 1.2 - 1.5x faster).  The
-// remaining misses are small block-structured inputs at fill 20 - 45, where
-// both kernels sit within 1.5 us of their launch cost.  The reference's 2.0
-// was the crossover of a T4, whose tensor cores are far less ahead of its
-// CUDA cores.
-constexpr float kHybridDefaultThreshold = 18.0f;
+// 256: any cut-off in 26 .. 32 loses 5.2% on average to the faster back end
+// (59 us in total); 18 loses 15.5% (394 us), 45 loses 3.2% but 208 us, most
+// of it on large uniform inputs at fill 33 - 50, where the CSR engine is up
+// to 2x faster.  The remaining misses are uniform inputs at fill 25 - 33,
+// within 15% either way, and partially filled blocks at fill 45, where the
+// MFMA kernel is 1.1 - 1.5x faster.  The reference's 2.0 was the crossover of
+// a T4, whose tensor cores are far less ahead of its CUDA cores.
+constexpr float kHybridDefaultThreshold = 32.0f;
 
 HybridPlan hybrid_choose(const CSR& h_A, int N,
                          float fill_in_threshold = kHybridDefaultThreshold);

@@ -187,10 +187,10 @@ def test_hybrid_choose_matches_oracle_rule(S, O):
             assert p.n_aligned == (N > 0 and N % 16 == 0)
             assert p.fill_in_ratio == pytest.approx(fill)
     assert S.backend_name(0) == "csr" and S.backend_name(1) == "wmma"
-    # the MI355X crossover: fill 18 (this matrix has fill ~6.6 -> matrix cores)
-    assert S.hybrid_default_threshold() == 18.0
+    # the MI355X crossover: fill 32 (this matrix has fill ~6.6 -> matrix cores)
+    assert S.hybrid_default_threshold() == 32.0
     p = S.hybrid_choose(A, 128)
-    assert p.threshold == 18.0 and p.backend_name == "wmma"
+    assert p.threshold == 32.0 and p.backend_name == "wmma"
 
 
 def test_nnz_balanced_bounds_equals_oracle(S, O):

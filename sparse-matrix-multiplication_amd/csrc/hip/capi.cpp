@@ -151,6 +151,8 @@ spmm::engine::EngineOpts opts_from_c(const spmm_engine_opts_t* o) {
         e.groups         = o->groups;
         e.slices         = o->slices;
         e.global_loads   = o->global_loads;
+        e.row_groups     = o->row_groups;
+        e.entry_lanes    = o->entry_lanes;
     }
     return e;
 }

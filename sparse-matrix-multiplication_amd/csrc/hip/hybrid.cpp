@@ -154,11 +154,24 @@ Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float
         // (power-law inputs) would leave their workgroups running long after
         // the rest, so then the engine runs the merge-path partition instead:
         // equal nonzero ranges per workgroup, long rows cut between them.
+        // Narrow B (N <= 64) or rows of a few entries, with no long row, go to
+        // the sub-wave row groups, which keep every lane busy there.
         DeviceCsrCopy csr;
         SPMM_TRY(upload_csr(h_A, csr));
         int max_row = 0;
         for (int r = 0; r < M; ++r) max_row = std::max(max_row, h_A.row_ptr[r + 1] - h_A.row_ptr[r]);
-        if (h_A.nnz == 0 || !split_pays(max_row)) {
+        const double avg_row = static_cast<double>(h_A.nnz) / M;
+        if (h_A.nnz > 0 && row_groups_pay(N, h_A.num_cols, avg_row, max_row)) {
+            // Narrow B or short rows without long ones: sub-wave row groups.
+            EngineOpts rg;
+            rg.row_groups = 1;
+            SPMM_TRY(time_median_launch(
+                [&] {
+                    return launch_csr(CsrRole::TiledV3, csr.view, d_B.as<float>(),
+                                      d_C.as<float>(), N, nullptr, nullptr, 0, &rg);
+                },
+                warmup, iters, ms));
+        } else if (h_A.nnz == 0 || !split_pays(max_row)) {
             SPMM_TRY(time_median_launch(
                 [&] {
                     return launch_csr(CsrRole::TiledV3, csr.view, d_B.as<float>(),

@@ -259,6 +259,74 @@ def test_tiled_v2_contract(S, torch, edge_cases):
     assert "N % 128" in str(e.value)
 
 
+def _run_opts(S, torch, A, B, opts):
+    dA = S.DeviceCSR(A)
+    dB = torch.from_numpy(B).cuda()
+    dC = torch.full((A.num_rows, B.shape[1]), float("nan"), device="cuda")
+    S.spmm_tiled_v3_opts(dA, dB, opts, dC)
+    torch.cuda.synchronize()
+    return dC.cpu().numpy()
+
+
+@pytest.mark.parametrize("vec", [0, 1, 2])
+@pytest.mark.parametrize("entry_lanes,unroll", [(0, 0), (1, 2), (4, 4), (64, 2)])
+def test_row_groups(S, torch, edge_cases, vec, entry_lanes, unroll):
+    # sub-wave row groups on every edge case: empty rows, duplicates, rows far
+    # longer than a group's share (the wave-wide pass), N from 1 to 520
+    opts = S.EngineOptsT(vec, 0, unroll, 0, 0, 0, 0, 1, entry_lanes)
+    for name, (A, B, C64, absC) in edge_cases.items():
+        say(f"csr row groups vec={vec} entry_lanes={entry_lanes} unroll={unroll} case={name}")
+        if B.shape[1] * 4 > 16383:
+            with pytest.raises(S.SpmmError):  # a B row no longer fits one buffer record
+                _run_opts(S, torch, A, B, opts)
+            continue
+        check_csr(_run_opts(S, torch, A, B, opts), C64, absC)
+
+
+@pytest.mark.parametrize("entry_lanes,unroll", [(8, 2), (2, 4), (16, 4)])
+def test_row_groups_long_row_boundary(S, O, torch, entry_lanes, unroll):
+    # N = 16 (four column lanes of 4 floats): a row longer than
+    # 8 * entry_lanes * unroll entries moves to the wave-wide pass; rows of
+    # that length -1 / +0 / +1 / x2, several long rows in one wave, empty rows,
+    # and a row count that is not a multiple of the rows per workgroup
+    rng = np.random.default_rng(entry_lanes * 10 + unroll)
+    cut = 8 * entry_lanes * unroll
+    lens = [cut - 1, cut, cut + 1, 2 * cut, cut + 1, 0, 3, cut + 5, 0, 2 * cut + 7, 1] * 3 + [cut + 2]
+    K = 4 * cut + 50
+    rows, cols = [], []
+    for r, n in enumerate(lens):
+        rows += [r] * n
+        cols += list(rng.choice(K, n, replace=False))
+    A = _coo_csr(S, len(lens), K, rows, cols, rng.uniform(-1, 1, len(rows)))
+    B = rng.uniform(-1, 1, (K, 16)).astype(np.float32)
+    C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)
+    say(f"csr row groups long-row boundary cut={cut} rows={len(lens)}")
+    C = _run_opts(S, torch, A, B, S.EngineOptsT(4, 0, unroll, 0, 0, 0, 0, 1, entry_lanes))
+    check_csr(C, C64, absC)
+
+
+@pytest.mark.parametrize("N", [1, 4, 16, 64])
+def test_row_groups_c2_narrow(S, O, torch, N):
+    # the c2 matrix at narrow B, where row groups are the hybrid's CSR choice;
+    # results are bitwise identical run to run
+    A, _ = make_config(S, "c2")
+    B = np.random.default_rng(N).uniform(-1, 1, (A.num_cols, N)).astype(np.float32)
+    C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=16)
+    opts = S.EngineOptsT(0, 0, 0, 0, 0, 0, 0, 1, 0)
+    say(f"csr row groups c2 N={N}")
+    C1 = _run_opts(S, torch, A, B, opts)
+    check_csr(C1, C64, absC)
+    C2 = _run_opts(S, torch, A, B, opts)
+    assert np.array_equal(C1.view(np.uint32), C2.view(np.uint32))
+
+
+def test_row_groups_argument_errors(S, torch, edge_cases):
+    A, B, _, _ = edge_cases["ragged"]
+    for lanes in (3, -2, 128):  # entry lanes: a power of two up to 64
+        with pytest.raises(S.SpmmError):
+            _run_opts(S, torch, A, B, S.EngineOptsT(0, 0, 0, 0, 0, 0, 0, 1, lanes))
+
+
 def test_launch_argument_errors(S, torch):
     s = S.CsrT(4, 4, 2, 0, 0, 0)  # nnz > 0 but null arrays
     rc = S.lib().spmm_c_tiled_v3(ctypes.byref(s), 1, 1, 8, None)

@@ -1,9 +1,10 @@
 """Seeded random parity sweep on cuda:0: random shapes, densities, row-length
-skew and engine options for the CSR engine (row partition and merge-path), and
-random shapes and kernel options for the MFMA BSR kernel, each checked against
-the CPU oracle with the same bars as the other GPU tests (fp32 CSR within
-1e-5 of the fp64 loop; fp16 BSR within 1e-2 of fp32 accumulation and within
-1e-5 of the exact product of the fp16 operands)."""
+skew and engine options for the CSR engine (row partition, merge-path and the
+sub-wave row groups), and random shapes and kernel options for the MFMA BSR
+kernel, each checked against the CPU oracle with the same bars as the other
+GPU tests (fp32 CSR within 1e-5 of the fp64 loop; fp16 BSR within 1e-2 of
+fp32 accumulation and within 1e-5 of the exact product of the fp16
+operands)."""
 import numpy as np
 import pytest
 
@@ -70,13 +71,14 @@ def test_csr_engine_random(S, O, torch, chunk):
         A = _random_csr(S, rng, M, K)
         B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
         opts = S.EngineOptsT(int(rng.choice([0, 1, 2, 4])), int(rng.choice([0, 2, 4, 8])),
-                             int(rng.choice([0, 4, 8])),
+                             int(rng.choice([0, 2, 4, 8])),
                              int(rng.choice([0, 0, 1, 3, 16, 64])),
                              int(rng.choice([0, 1, 2, 4, 8])), int(rng.choice([0, 1, 2, 4, 8])),
-                             int(rng.choice([0, 0, 1])))
+                             int(rng.choice([0, 0, 1])), int(rng.choice([0, 0, 1])),
+                             int(rng.choice([0, 1, 2, 8, 64])))
         say(f"fuzz csr chunk={chunk} case={case} M={M} K={K} N={N} nnz={A.nnz} "
             f"opts=({opts.vec},{opts.waves},{opts.unroll},{opts.rows_per_block},{opts.groups},"
-            f"{opts.slices},{opts.global_loads})")
+            f"{opts.slices},{opts.global_loads},{opts.row_groups},{opts.entry_lanes})")
         C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)
         dA = S.DeviceCSR(A)
         dB = torch.from_numpy(B).cuda()

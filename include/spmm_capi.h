@@ -91,10 +91,12 @@ typedef struct spmm_engine_opts_t {
     int slices;         /* XCD-tied column slices of B and C: 1, 2, 4, 8 */
     int global_loads;   /* 1: 64-bit address loads of B instead of buffer loads
                            (automatic when B exceeds 2 GiB or N > 4095) */
-    int row_groups;     /* 1: sub-wave row groups instead of the row-block engine:
+    int row_groups;     /* sub-wave row groups instead of the row-block engine:
                            one row per group of column lanes x entry lanes, no
                            partition, buffer loads only (N <= 4095, B < 2 GiB);
-                           vec as above, unroll 2 or 4 */
+                           vec as above, unroll 2 or 4.  1: index-load form
+                           chosen from the shape, 2: per-lane index loads,
+                           3: cooperative index loads */
     int entry_lanes;    /* row groups: entry lanes per row, power of two <= 64 */
 } spmm_engine_opts_t;
 

@@ -520,9 +520,11 @@ __global__ __launch_bounds__(256) void csr_split_fixup(const int* __restrict__ r
 // rows of 1 .. 300 entries, up to 2x at N = 64, and for N = 128 / 256 on rows
 // of a few entries.
 //
-// A row longer than 8 iterations of its group (8 * LE * U entries) is not
-// taken by the group but by the whole wave afterwards (64 / LC entry lanes),
-// so one long row delays only its own wave.  Rows far longer than that belong
+// A row longer than 8 iterations of its group (8 * LE * U entries) and than
+// 4x the average row is not taken by the group but by the whole wave
+// afterwards (64 / LC entry lanes), so one long row delays only its own wave
+// and is taken by 64 / L times the lanes.  (Rows of about average length stay
+// in their groups: moving them would only serialise the wave's rows.)  Rows far longer than that belong
 // to the engine or the merge-path partition, which share a row between waves
 // and workgroups; the dispatch rule below keeps them there.
 // ---------------------------------------------------------------------------
@@ -535,8 +537,9 @@ struct RowGroupArgs {
     int          M;
     int          N;
     int          K;
-    int          lc_log;  // column lanes per row: 1 << lc_log
-    int          le_log;  // entry lanes per row: 1 << le_log
+    int          lc_log;    // column lanes per row: 1 << lc_log
+    int          le_log;    // entry lanes per row: 1 << le_log
+    int          long_len;  // rows with more entries go to the wave-wide pass
 };
 
 template <int VEC>
@@ -577,7 +580,47 @@ __device__ __forceinline__ typename Vec<VEC>::T row_segment_sum(
     return acc;
 }
 
+// Cooperative form of a group's pass over entries [p0, p1): the L lanes of
+// the group (lanes g0 .. g0+L-1, this lane gl) load L consecutive entries with
+// one coalesced load for the columns and one for the values, and sub-step j
+// hands entry j*LE + e to lane (e, c) with a shuffle -- one load per L entries
+// instead of one per entry lane and entry.
 template <int VEC, int U>
+__device__ __forceinline__ typename Vec<VEC>::T row_chunks_sum(
+    const RowGroupArgs& a, __amdgpu_buffer_rsrc_t rb, int p0, int p1, int g0, int gl, int e,
+    int L, int LE, int colb) {
+    using VT = typename Vec<VEC>::T;
+    VT acc = vzero<VEC>();
+    const int sub = L / LE;  // sub-steps per chunk (= column lanes)
+    for (int base = p0; base < p1; base += L) {
+        const int   q   = base + gl;
+        const int   kc  = q < p1 ? a.col_idx[q] : -1;
+        const float vc  = q < p1 ? a.vals[q] : 0.0f;
+        const int   cnt = min(L, p1 - base);
+        for (int j0 = 0; j0 < sub && j0 * LE < cnt; j0 += U) {
+            int   ks[U];
+            float vs[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int src = g0 + (((j0 + u) * LE + e) & (L - 1));
+                ks[u] = __shfl(kc, src);
+                vs[u] = __shfl(vc, src);
+                if (j0 + u >= sub) {
+                    ks[u] = -1;
+                    vs[u] = 0.0f;
+                }
+            }
+            VT bs[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) bs[u] = load_b<VEC, true>(rb, nullptr, ks[u], colb, a.N);
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc += vs[u] * bs[u];
+        }
+    }
+    return acc;
+}
+
+template <int VEC, int U, bool COOP>
 __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
     using VT = typename Vec<VEC>::T;
     const int LC   = 1 << a.lc_log;
@@ -595,7 +638,7 @@ __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
         start = a.row_ptr[row];
         end   = a.row_ptr[row + 1];
     }
-    const bool is_long = end - start > 8 * LE * U;
+    const bool is_long = end - start > a.long_len;
     const int  g_end   = is_long ? start : end;
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(a.B), static_cast<short>(a.N * 4), a.K, kBufWord3);
@@ -603,7 +646,13 @@ __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
     for (int n0 = 0; n0 < a.N; n0 += LC * VEC) {
         const int  n    = n0 + c * VEC;
         const bool col  = n < a.N;  // lanes past N read column 0 and store nothing
-        VT acc = row_segment_sum<VEC, U>(a, rb, start + e, g_end, LE, col ? n * 4 : 0);
+        VT acc;
+        if constexpr (COOP) {
+            acc = row_chunks_sum<VEC, U>(a, rb, start, g_end, lane & ~(L - 1), gl, e, L, LE,
+                                         col ? n * 4 : 0);
+        } else {
+            acc = row_segment_sum<VEC, U>(a, rb, start + e, g_end, LE, col ? n * 4 : 0);
+        }
         for (int m = LC; m < L; m <<= 1) acc = xor_add<VEC>(acc, m);
         if (live && !is_long && e == 0 && col) {
             store_vec<VEC>(a.C + static_cast<size_t>(row) * a.N + n, acc);
@@ -622,7 +671,13 @@ __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
         for (int n0 = 0; n0 < a.N; n0 += LC * VEC) {
             const int  n   = n0 + c * VEC;
             const bool col = n < a.N;
-            VT acc = row_segment_sum<VEC, U>(a, rb, rs + we, re, kWave / LC, col ? n * 4 : 0);
+            VT acc;
+            if constexpr (COOP) {
+                acc = row_chunks_sum<VEC, U>(a, rb, rs, re, 0, lane, we, kWave, kWave / LC,
+                                             col ? n * 4 : 0);
+            } else {
+                acc = row_segment_sum<VEC, U>(a, rb, rs + we, re, kWave / LC, col ? n * 4 : 0);
+            }
             for (int m = LC; m < kWave; m <<= 1) acc = xor_add<VEC>(acc, m);
             if (we == 0 && col) store_vec<VEC>(a.C + static_cast<size_t>(r) * a.N + n, acc);
         }
@@ -744,27 +799,61 @@ int pow2_log_at_least(int x) {
     return l;
 }
 
-template <int VEC>
+// Column lanes (log2) of a row group: enough to cover N in one pass, at most
+// 64; 32 or 64 drop to 16 (two or four column passes) while the matrix would
+// still give >= 16384 waves.
+constexpr long kRowGroupTargetWaves = 8192;
+int row_group_lc_log(int M, int N, int vec) {
+    int lc_log = pow2_log_at_least(ceil_div(N, vec));
+    while (lc_log > 4 && (static_cast<long>(M) << lc_log) / kWave >= 2 * kRowGroupTargetWaves) {
+        --lc_log;
+    }
+    return lc_log;
+}
+
+template <int VEC, bool COOP>
 hipError_t run_row_groups(const RowGroupArgs& args, int unroll, int grid, hipStream_t stream) {
     if (unroll == 4) {
-        hipLaunchKernelGGL((csr_row_groups<VEC, 4>), dim3(grid), dim3(256), 0, stream, args);
+        hipLaunchKernelGGL((csr_row_groups<VEC, 4, COOP>), dim3(grid), dim3(256), 0, stream, args);
     } else {
-        hipLaunchKernelGGL((csr_row_groups<VEC, 2>), dim3(grid), dim3(256), 0, stream, args);
+        hipLaunchKernelGGL((csr_row_groups<VEC, 2, COOP>), dim3(grid), dim3(256), 0, stream, args);
     }
     return hipGetLastError();
 }
 
+template <int VEC>
+hipError_t run_row_groups(const RowGroupArgs& args, bool coop, int unroll, int grid,
+                          hipStream_t stream) {
+    return coop ? run_row_groups<VEC, true>(args, unroll, grid, stream)
+                : run_row_groups<VEC, false>(args, unroll, grid, stream);
+}
+
 // Shape of the sub-wave row groups, measured on MI355X over uniform rows of
-// 1 .. 300 entries, M = 2048 .. 32768 and N = 1 .. 256 (within 5% of the best
-// shape on average): column lanes cover N in one pass (up to 64 lanes), entry
-// lanes ~1.5 * sqrt(average row) rounded to a power of two (fewer lanes per
-// row for short rows: more rows per wave), 4 entries per entry lane per
-// iteration from 32 entries per row on, else 2.
+// 1 .. 300 entries, M = 2048 .. 65536 and N = 1 .. 256:
+//  - column lanes cover N in one pass (up to 64 lanes), except that 32 or 64
+//    column lanes drop to 16 (two or four passes) while the matrix would
+//    still give >= 16384 waves (e.g. M = 32768, N = 128: 96 -> 89 us);
+//  - entry lanes ~1.5 * sqrt(average row) as a power of two, but no more than
+//    keep the grid near 8192 waves (32 per CU): beyond that, more rows per
+//    wave beat more lanes per row;
+//  - 4 entries per entry lane per iteration from 32 entries per row on while
+//    B is at most 2 MiB (latency-bound: few, long rows), else 2 -- with B
+//    beyond one XCD's L2, fewer gathers in flight keep more of it cached
+//    (M = 32768, N = 128, 82 entries per row: 123 -> 88 us);
+//  - the cooperative loads (one column/value load per L entries, handed out
+//    by shuffles) from 4 column lanes on when rows average >= 32 entries or
+//    column lanes x rows >= 2^18: redundant per-lane index loads then cost
+//    more than the shuffles (M = 8192, N = 64, 82 per row: 11.4 -> 9.1 us;
+//    M = 32768, N = 128: 119 -> 87 us); on short rows of a smaller matrix the
+//    per-lane loads are 5-15% ahead.
+// row_groups: 1 picks the load form by that rule, 2 forces per-lane loads,
+// 3 forces the cooperative loads.
 Error launch_row_groups(const CSR& A, const float* B, float* C, int N, hipStream_t stream,
                         int vec, const EngineOpts& o) {
+    constexpr long kTargetWaves = kRowGroupTargetWaves;
     const int M = A.num_rows;
     const double avg = A.nnz > 0 ? static_cast<double>(A.nnz) / M : 0.0;
-    const int lc_log = pow2_log_at_least(ceil_div(N, vec));
+    const int lc_log = row_group_lc_log(M, N, vec);
     int le_log;
     if (o.entry_lanes != 0) {
         if (o.entry_lanes < 0 || o.entry_lanes > 64 || (o.entry_lanes & (o.entry_lanes - 1)) != 0) {
@@ -774,16 +863,30 @@ Error launch_row_groups(const CSR& A, const float* B, float* C, int N, hipStream
     } else {
         const double want = 1.5 * std::sqrt(std::max(avg, 1.0));
         le_log = static_cast<int>(std::lround(std::log2(want)));
+        const long cap = kTargetWaves * kWave / std::max(1L, static_cast<long>(M) << lc_log);
+        int cap_log = 0;
+        while ((2L << cap_log) <= cap) ++cap_log;
+        le_log = std::min(le_log, cap_log);
     }
     le_log = std::max(0, std::min(le_log, 6 - lc_log));
-    const int unroll = (o.unroll == 2 || o.unroll == 4) ? o.unroll : (avg >= 32.0 ? 4 : 2);
+    const bool b_small = static_cast<long long>(A.num_cols) * N * 4 <= (2LL << 20);
+    const int unroll = (o.unroll == 2 || o.unroll == 4) ? o.unroll
+                                                        : ((avg >= 32.0 && b_small) ? 4 : 2);
+    bool coop;
+    if (o.row_groups == 2) coop = false;
+    else if (o.row_groups == 3) coop = true;
+    else coop = lc_log >= 2 && (avg >= 32.0 || (static_cast<long>(M) << lc_log) >= (1L << 18));
     const int rows_per_wg = 4 * (kWave >> (lc_log + le_log));
     const int grid = ceil_div(M, rows_per_wg);
-    RowGroupArgs args{A.row_ptr, A.col_idx, A.values, B, C, M, N, A.num_cols, lc_log, le_log};
+    const int long_len = std::max(8 << le_log << (unroll == 4 ? 2 : 1),
+                                  static_cast<int>(std::ceil(std::min(4.0 * avg, 1.0e9))));
+    RowGroupArgs args{A.row_ptr, A.col_idx,  A.values, B,       C,
+                      M,         N,          A.num_cols, lc_log, le_log,
+                      long_len};
     hipError_t e;
-    if (vec == 4) e = run_row_groups<4>(args, unroll, grid, stream);
-    else if (vec == 2) e = run_row_groups<2>(args, unroll, grid, stream);
-    else e = run_row_groups<1>(args, unroll, grid, stream);
+    if (vec == 4) e = run_row_groups<4>(args, coop, unroll, grid, stream);
+    else if (vec == 2) e = run_row_groups<2>(args, coop, unroll, grid, stream);
+    else e = run_row_groups<1>(args, coop, unroll, grid, stream);
     return from_hip(e, "csr row groups launch");
 }
 
@@ -844,7 +947,10 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
         return fail(kInvalid, "engine vec must be 1, 2 or 4");
     }
     const int vec = pick_vec(N, B, C, want_vec);
-    if (o.row_groups == 1) {
+    if (o.row_groups != 0) {
+        if (o.row_groups < 0 || o.row_groups > 3) {
+            return fail(kInvalid, "row_groups must be 0 (engine), 1 (auto), 2 or 3");
+        }
         if (bounds != nullptr || split != nullptr) {
             return fail(kInvalid, "row groups take no explicit partition");
         }
@@ -934,19 +1040,19 @@ bool split_pays(int max_row_nnz) {
     return max_row_nnz > 4 * 640;
 }
 
-bool row_groups_pay(int N, int K, double avg_row, int max_row) {
+bool row_groups_pay(int M, int N, int K, double avg_row, int max_row) {
     // Measured on MI355X against the row-block engine (uniform rows of 1 ..
-    // 300 entries, M = 2048 .. 32768): row groups win 1.5 - 4x for N <= 32,
-    // up to 2x for N = 64 on rows of up to ~160 entries, and at N = 128 / 256
-    // while N * avg_row <= 2048 (rows of 16 / 8 entries).  A row longer than
-    // 4096 / column-lanes entries would keep one wave busy for more than 16
-    // iterations of its wave-wide pass: then the engine, which shares long
-    // rows between waves, is the safer choice.
-    if (N <= 0 || !b_fits_buffer(K, N)) return false;
+    // 300 entries, M = 2048 .. 65536): row groups win 1.5 - 4x for N <= 32,
+    // 1.1 - 1.9x for N = 64, at N = 128 on matrices of >= 16384 rows
+    // (1.04 - 1.3x) or rows of <= 16 entries, and at N = 256 on rows of <= 8
+    // entries.  A row longer than 4096 / column-lanes entries would keep one
+    // wave busy for more than 16 iterations of its wave-wide pass: then the
+    // engine, which shares long rows between waves, is the safer choice.
+    if (N <= 0 || M <= 0 || !b_fits_buffer(K, N)) return false;
     const int vec = N % 4 == 0 ? 4 : (N % 2 == 0 ? 2 : 1);
-    const int lc  = 1 << pow2_log_at_least((N + vec - 1) / vec);
+    const int lc  = 1 << row_group_lc_log(M, N, vec);
     if (max_row > 4096 / lc) return false;
-    return N <= 32 || (N <= 64 && avg_row <= 160.0) || N * avg_row <= 2048.0;
+    return N <= 64 || (N <= 128 && M >= 16384) || N * avg_row <= 2048.0;
 }
 
 Error launch_csr_split(const CSR& A, const float* B, float* C, int N, hipStream_t stream,

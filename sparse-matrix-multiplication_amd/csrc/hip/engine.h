@@ -43,9 +43,11 @@ struct EngineOpts {
     int groups         = 0;  // lane groups per wave (entries interleaved): 1, 2 or 4
     int slices         = 0;  // XCD-tied column slices of B and C: 1, 2, 4 or 8
     int global_loads   = 0;  // 1: 64-bit address loads of B instead of buffer loads
-    // 1: sub-wave row groups instead of the row-block engine (one row per
-    // group of column lanes x entry lanes; no partition, buffer loads only;
-    // unroll 2 or 4 entries per entry lane per iteration, vec as above).
+    // Sub-wave row groups instead of the row-block engine (one row per group
+    // of column lanes x entry lanes; no partition, buffer loads only; unroll
+    // 2 or 4 entries per entry lane per iteration, vec as above): 1 with the
+    // index-load form chosen from the shape, 2 per-lane index loads, 3
+    // cooperative index loads handed out by shuffles.
     int row_groups     = 0;
     int entry_lanes    = 0;  // row groups: entry lanes per row, a power of two up to 64
 };
@@ -118,9 +120,9 @@ Error launch_csr_split(const CSR& d_A, const float* d_B, float* d_C, int N, hipS
 int split_partition_parts(int nnz);
 bool split_pays(int max_row_nnz);
 
-// Whether sub-wave row groups beat the row-block engine for N columns of a
-// K-row B, rows of avg_row entries on average and at most max_row.
-bool row_groups_pay(int N, int K, double avg_row, int max_row);
+// Whether sub-wave row groups beat the row-block engine for an M-row CSR with
+// rows of avg_row entries on average and at most max_row, times a K x N B.
+bool row_groups_pay(int M, int N, int K, double avg_row, int max_row);
 
 // Number of workgroups the engine uses for an explicit partition of this CSR.
 int default_partition_parts(int num_rows, int nnz);

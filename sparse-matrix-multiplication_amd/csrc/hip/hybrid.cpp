@@ -161,7 +161,7 @@ Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float
         int max_row = 0;
         for (int r = 0; r < M; ++r) max_row = std::max(max_row, h_A.row_ptr[r + 1] - h_A.row_ptr[r]);
         const double avg_row = static_cast<double>(h_A.nnz) / M;
-        if (h_A.nnz > 0 && row_groups_pay(N, h_A.num_cols, avg_row, max_row)) {
+        if (h_A.nnz > 0 && row_groups_pay(M, N, h_A.num_cols, avg_row, max_row)) {
             // Narrow B or short rows without long ones: sub-wave row groups.
             EngineOpts rg;
             rg.row_groups = 1;

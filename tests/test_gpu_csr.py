@@ -268,14 +268,17 @@ def _run_opts(S, torch, A, B, opts):
     return dC.cpu().numpy()
 
 
+@pytest.mark.parametrize("form", [1, 2, 3])
 @pytest.mark.parametrize("vec", [0, 1, 2])
 @pytest.mark.parametrize("entry_lanes,unroll", [(0, 0), (1, 2), (4, 4), (64, 2)])
-def test_row_groups(S, torch, edge_cases, vec, entry_lanes, unroll):
+def test_row_groups(S, torch, edge_cases, form, vec, entry_lanes, unroll):
     # sub-wave row groups on every edge case: empty rows, duplicates, rows far
-    # longer than a group's share (the wave-wide pass), N from 1 to 520
-    opts = S.EngineOptsT(vec, 0, unroll, 0, 0, 0, 0, 1, entry_lanes)
+    # longer than a group's share (the wave-wide pass), N from 1 to 520; form
+    # 2 = per-lane index loads, 3 = cooperative index loads, 1 = chosen
+    opts = S.EngineOptsT(vec, 0, unroll, 0, 0, 0, 0, form, entry_lanes)
     for name, (A, B, C64, absC) in edge_cases.items():
-        say(f"csr row groups vec={vec} entry_lanes={entry_lanes} unroll={unroll} case={name}")
+        say(f"csr row groups form={form} vec={vec} entry_lanes={entry_lanes} unroll={unroll} "
+            f"case={name}")
         if B.shape[1] * 4 > 16383:
             with pytest.raises(S.SpmmError):  # a B row no longer fits one buffer record
                 _run_opts(S, torch, A, B, opts)
@@ -283,15 +286,19 @@ def test_row_groups(S, torch, edge_cases, vec, entry_lanes, unroll):
         check_csr(_run_opts(S, torch, A, B, opts), C64, absC)
 
 
+@pytest.mark.parametrize("form", [2, 3])
 @pytest.mark.parametrize("entry_lanes,unroll", [(8, 2), (2, 4), (16, 4)])
-def test_row_groups_long_row_boundary(S, O, torch, entry_lanes, unroll):
+def test_row_groups_long_row_boundary(S, O, torch, form, entry_lanes, unroll):
     # N = 16 (four column lanes of 4 floats): a row longer than
-    # 8 * entry_lanes * unroll entries moves to the wave-wide pass; rows of
+    # 8 * entry_lanes * unroll entries (and 4x the average row, which the
+    # 300 one-entry rows keep below that) moves to the wave-wide pass; rows of
     # that length -1 / +0 / +1 / x2, several long rows in one wave, empty rows,
     # and a row count that is not a multiple of the rows per workgroup
     rng = np.random.default_rng(entry_lanes * 10 + unroll)
     cut = 8 * entry_lanes * unroll
     lens = [cut - 1, cut, cut + 1, 2 * cut, cut + 1, 0, 3, cut + 5, 0, 2 * cut + 7, 1] * 3 + [cut + 2]
+    lens += [1] * 300
+    assert 4.0 * sum(lens) / len(lens) < cut
     K = 4 * cut + 50
     rows, cols = [], []
     for r, n in enumerate(lens):
@@ -300,8 +307,8 @@ def test_row_groups_long_row_boundary(S, O, torch, entry_lanes, unroll):
     A = _coo_csr(S, len(lens), K, rows, cols, rng.uniform(-1, 1, len(rows)))
     B = rng.uniform(-1, 1, (K, 16)).astype(np.float32)
     C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)
-    say(f"csr row groups long-row boundary cut={cut} rows={len(lens)}")
-    C = _run_opts(S, torch, A, B, S.EngineOptsT(4, 0, unroll, 0, 0, 0, 0, 1, entry_lanes))
+    say(f"csr row groups long-row boundary form={form} cut={cut} rows={len(lens)}")
+    C = _run_opts(S, torch, A, B, S.EngineOptsT(4, 0, unroll, 0, 0, 0, 0, form, entry_lanes))
     check_csr(C, C64, absC)
 
 
@@ -320,11 +327,27 @@ def test_row_groups_c2_narrow(S, O, torch, N):
     assert np.array_equal(C1.view(np.uint32), C2.view(np.uint32))
 
 
+@pytest.mark.parametrize("N", [64, 128, 256])
+def test_row_groups_tall(S, O, torch, N):
+    # 32768 rows: the column lanes drop to 16 (several column passes), the
+    # entry lanes follow the wave target and the cooperative loads are chosen
+    A = S.generate_uniform_random_csr(32768, 32768, 16.0 / 32768, 91)
+    B = np.random.default_rng(N + 1).uniform(-1, 1, (32768, N)).astype(np.float32)
+    C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=16)
+    for form in (1, 2, 3):
+        say(f"csr row groups tall M=32768 N={N} form={form}")
+        check_csr(_run_opts(S, torch, A, B, S.EngineOptsT(0, 0, 0, 0, 0, 0, 0, form, 0)),
+                  C64, absC)
+
+
 def test_row_groups_argument_errors(S, torch, edge_cases):
     A, B, _, _ = edge_cases["ragged"]
     for lanes in (3, -2, 128):  # entry lanes: a power of two up to 64
         with pytest.raises(S.SpmmError):
             _run_opts(S, torch, A, B, S.EngineOptsT(0, 0, 0, 0, 0, 0, 0, 1, lanes))
+    for form in (-1, 4):  # 0 engine, 1 chosen, 2 per-lane loads, 3 cooperative loads
+        with pytest.raises(S.SpmmError):
+            _run_opts(S, torch, A, B, S.EngineOptsT(0, 0, 0, 0, 0, 0, 0, form, 0))
 
 
 def test_launch_argument_errors(S, torch):

@@ -74,7 +74,7 @@ def test_csr_engine_random(S, O, torch, chunk):
                              int(rng.choice([0, 2, 4, 8])),
                              int(rng.choice([0, 0, 1, 3, 16, 64])),
                              int(rng.choice([0, 1, 2, 4, 8])), int(rng.choice([0, 1, 2, 4, 8])),
-                             int(rng.choice([0, 0, 1])), int(rng.choice([0, 0, 1])),
+                             int(rng.choice([0, 0, 1])), int(rng.choice([0, 0, 1, 2, 3])),
                              int(rng.choice([0, 1, 2, 8, 64])))
         say(f"fuzz csr chunk={chunk} case={case} M={M} K={K} N={N} nnz={A.nnz} "
             f"opts=({opts.vec},{opts.waves},{opts.unroll},{opts.rows_per_block},{opts.groups},"

@@ -11,8 +11,9 @@ roofline.achieved = compulsory bytes per launch (scripts/roofline.py:177-185:
 8*nnz + 4*(M+1) + 4*K*N + 4*M*N) / average launch time.  roofline.traffic is the
 HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
 scaled by the copy-kernel calibration), read from profiles/traffic_c2.json when
-present.  cpu_baseline times the CPU oracle's fp64 loop (oracle/) on the same
-matrix on the host cores.
+present.  roofline.measured_copy is the rate a 256 MiB device-to-device copy
+reaches on the same GPU, with achieved / that rate.  cpu_baseline times the CPU
+oracle's fp64 loop (oracle/) on the same matrix on the host cores.
 """
 from __future__ import annotations
 
@@ -56,6 +57,27 @@ def cpu_baseline(A, B, flops: float, budget_s: float = 12.0):
     return {"value": flops / med / 1e9, "unit": "GFLOP/s", "cores": threads, "kind": "port",
             "sample": f"full c2 workload (oracle fp64 CSR x dense, {threads} threads), "
                       f"median of {len(times)} runs, {med * 1e3:.2f} ms each"}
+
+
+def measured_copy_gbs(torch, stream, reps: int = 20) -> float:
+    """HBM rate a plain 256 MiB device-to-device copy reaches on this GPU
+    (read + write bytes per second): the measured counterpart of the 8 TB/s
+    datasheet peak, reported beside it."""
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / reps
+    del src, dst
+    return 2.0 * COPY_BYTES / sec / 1e9
 
 
 def copy_calibration(steps: int) -> int:
@@ -124,6 +146,8 @@ def main() -> int:
     alg_bytes = 8.0 * nnz + 4.0 * (m + 1) + 4.0 * k * n + 4.0 * m * n
     achieved = alg_bytes / (ms * 1e-3) / 1e9
 
+    copy_gbs = measured_copy_gbs(torch, stream)
+
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_c2.json")
     if os.path.exists(tpath):
@@ -146,7 +170,11 @@ def main() -> int:
         "config": dict(WORKLOAD, nnz=nnz),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic},
+                     "traffic": traffic,
+                     "measured_copy": {"value": round(copy_gbs, 1), "unit": "GB/s",
+                                       "frac": round(achieved / copy_gbs, 4),
+                                       "what": "256 MiB device-to-device copy on this GPU, "
+                                               "read + write bytes / time"}},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(A, B, flops)

@@ -96,7 +96,10 @@ typedef struct spmm_engine_opts_t {
                            partition, buffer loads only (N <= 4095, B < 2 GiB);
                            vec as above, unroll 2 or 4.  1: index-load form
                            chosen from the shape, 2: per-lane index loads,
-                           3: cooperative index loads */
+                           3: cooperative index loads.  0: the engine, except
+                           that default launches of tiled_v3 / tiled_v4 with
+                           N <= 8 (at most two 16-byte column lanes) take the
+                           row groups */
     int entry_lanes;    /* row groups: entry lanes per row, power of two <= 64 */
 } spmm_engine_opts_t;
 

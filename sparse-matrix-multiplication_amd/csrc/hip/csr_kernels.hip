@@ -947,6 +947,23 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
         return fail(kInvalid, "engine vec must be 1, 2 or 4");
     }
     const int vec = pick_vec(N, B, C, want_vec);
+    // Default launches of the production roles at N of a few columns (at most
+    // two column lanes of VEC floats, e.g. N <= 8 with 16-byte lanes) take the
+    // sub-wave row groups: the engine keeps 3/4 or more of its lanes idle
+    // there, and with 32 or 64 entry lanes the row groups' wave-wide pass still
+    // shares a long row among many lanes (measured on MI355X: 1.6 - 3.4x
+    // faster on uniform rows, 1.5 - 3x on power-law rows of up to 4096
+    // entries).  Any explicit engine option keeps the engine.
+    const bool engine_defaults = o.vec == 0 && o.waves == 0 && o.unroll == 0 &&
+                                 o.rows_per_block == 0 && o.groups == 0 && o.slices == 0 &&
+                                 o.global_loads == 0 && o.entry_lanes == 0;
+    if (o.row_groups == 0 && engine_defaults && bounds == nullptr && split == nullptr &&
+        (role == CsrRole::TiledV3 || role == CsrRole::TiledV4) &&
+        b_fits_buffer(A.num_cols, N) && pow2_log_at_least(ceil_div(N, vec)) <= 1) {
+        EngineOpts rg = o;
+        rg.row_groups = 1;
+        return launch_row_groups(A, B, C, N, stream, vec, rg);
+    }
     if (o.row_groups != 0) {
         if (o.row_groups < 0 || o.row_groups > 3) {
             return fail(kInvalid, "row_groups must be 0 (engine), 1 (auto), 2 or 3");

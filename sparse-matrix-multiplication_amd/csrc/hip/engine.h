@@ -47,7 +47,9 @@ struct EngineOpts {
     // of column lanes x entry lanes; no partition, buffer loads only; unroll
     // 2 or 4 entries per entry lane per iteration, vec as above): 1 with the
     // index-load form chosen from the shape, 2 per-lane index loads, 3
-    // cooperative index loads handed out by shuffles.
+    // cooperative index loads handed out by shuffles.  0: the engine, except
+    // that default launches of spmm_tiled_v3 / _v4 with at most two column
+    // lanes (N <= 8 with 16-byte lanes) take the row groups.
     int row_groups     = 0;
     int entry_lanes    = 0;  // row groups: entry lanes per row, a power of two up to 64
 };

@@ -540,6 +540,9 @@ struct RowGroupArgs {
     int          lc_log;    // column lanes per row: 1 << lc_log
     int          le_log;    // entry lanes per row: 1 << le_log
     int          long_len;  // rows with more entries go to the wave-wide pass
+    int          slices;    // XCD-tied column slices: 1, 2, 4 or 8
+    int          slice_cols;
+    int          nblocks;   // row blocks (workgroups of one column slice)
 };
 
 template <int VEC>
@@ -631,7 +634,20 @@ __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
     const int gl   = lane & (L - 1);
     const int c    = gl & (LC - 1);
     const int e    = gl >> a.lc_log;
-    const int row  = (blockIdx.x * 4 + wave) * (kWave / L) + (lane >> (a.lc_log + a.le_log));
+    // Column slices tied to XCDs as in the engine: workgroup g runs on XCD
+    // g % 8, and with S slices XCDs s*8/S .. (s+1)*8/S - 1 compute columns
+    // [s*SC, (s+1)*SC) of every row block, so each XCD's L2 holds 1/S of B.
+    int rblk = blockIdx.x, slice = 0;
+    if (a.slices > 1) {
+        const int per = 8 / a.slices;
+        const int x   = blockIdx.x & 7;
+        rblk  = (blockIdx.x >> 3) * per + x % per;
+        slice = x / per;
+    }
+    if (rblk >= a.nblocks) return;  // whole workgroup; no barrier or shuffle follows it
+    const int cbeg = slice * a.slice_cols;
+    const int cend = min(a.N, cbeg + a.slice_cols);
+    const int row  = (rblk * 4 + wave) * (kWave / L) + (lane >> (a.lc_log + a.le_log));
     const bool live = row < a.M;
     int start = 0, end = 0;
     if (live) {
@@ -643,9 +659,9 @@ __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(a.B), static_cast<short>(a.N * 4), a.K, kBufWord3);
 
-    for (int n0 = 0; n0 < a.N; n0 += LC * VEC) {
+    for (int n0 = cbeg; n0 < cend; n0 += LC * VEC) {
         const int  n    = n0 + c * VEC;
-        const bool col  = n < a.N;  // lanes past N read column 0 and store nothing
+        const bool col  = n < cend;  // lanes past the slice read column 0 and store nothing
         VT acc;
         if constexpr (COOP) {
             acc = row_chunks_sum<VEC, U>(a, rb, start, g_end, lane & ~(L - 1), gl, e, L, LE,
@@ -668,9 +684,9 @@ __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
         const int r  = __shfl(row, src);
         const int rs = __shfl(start, src);
         const int re = __shfl(end, src);
-        for (int n0 = 0; n0 < a.N; n0 += LC * VEC) {
+        for (int n0 = cbeg; n0 < cend; n0 += LC * VEC) {
             const int  n   = n0 + c * VEC;
-            const bool col = n < a.N;
+            const bool col = n < cend;
             VT acc;
             if constexpr (COOP) {
                 acc = row_chunks_sum<VEC, U>(a, rb, rs, re, 0, lane, we, kWave, kWave / LC,
@@ -811,6 +827,21 @@ int row_group_lc_log(int M, int N, int vec) {
     return lc_log;
 }
 
+// XCD-tied column slices of the row groups: on rows of up to 24 entries with
+// a B larger than one XCD's 4 MiB L2, the fewest slices (a power of two, at
+// most 8, each at least 32 columns wide) that bring an XCD's share of B under
+// 4 MiB (measured on MI355X: M = 16384, N = 256, 16 per row 28.4 -> 20.2 us
+// with 4 slices; M = 32768, N = 128: 28.5 -> 25.0 us).  Longer rows keep one
+// slice: every slice re-reads the rows' column indices, which then costs more
+// than the L2 misses it saves.
+int row_group_slices(int K, int N, double avg_row) {
+    if (avg_row > 24.0) return 1;
+    const long long b_bytes = static_cast<long long>(K) * N * 4;
+    int s = 1;
+    while (s < 8 && b_bytes > (4LL << 20) * s && N / (2 * s) >= 32) s *= 2;
+    return s;
+}
+
 template <int VEC, bool COOP>
 hipError_t run_row_groups(const RowGroupArgs& args, int unroll, int grid, hipStream_t stream) {
     if (unroll == 4) {
@@ -853,7 +884,11 @@ Error launch_row_groups(const CSR& A, const float* B, float* C, int N, hipStream
     constexpr long kTargetWaves = kRowGroupTargetWaves;
     const int M = A.num_rows;
     const double avg = A.nnz > 0 ? static_cast<double>(A.nnz) / M : 0.0;
-    const int lc_log = row_group_lc_log(M, N, vec);
+    int slices = o.slices;
+    if (slices == 0) slices = row_group_slices(A.num_cols, N, avg);
+    if (slices != 1 && slices != 2 && slices != 4 && slices != 8) slices = 1;
+    const int slice_cols = ceil_div(ceil_div(N, slices), vec) * vec;
+    const int lc_log = row_group_lc_log(M, slice_cols, vec);
     int le_log;
     if (o.entry_lanes != 0) {
         if (o.entry_lanes < 0 || o.entry_lanes > 64 || (o.entry_lanes & (o.entry_lanes - 1)) != 0) {
@@ -863,7 +898,8 @@ Error launch_row_groups(const CSR& A, const float* B, float* C, int N, hipStream
     } else {
         const double want = 1.5 * std::sqrt(std::max(avg, 1.0));
         le_log = static_cast<int>(std::lround(std::log2(want)));
-        const long cap = kTargetWaves * kWave / std::max(1L, static_cast<long>(M) << lc_log);
+        const long cap =
+            kTargetWaves * kWave / std::max(1L, (static_cast<long>(M) << lc_log) * slices);
         int cap_log = 0;
         while ((2L << cap_log) <= cap) ++cap_log;
         le_log = std::min(le_log, cap_log);
@@ -877,12 +913,13 @@ Error launch_row_groups(const CSR& A, const float* B, float* C, int N, hipStream
     else if (o.row_groups == 3) coop = true;
     else coop = lc_log >= 2 && (avg >= 32.0 || (static_cast<long>(M) << lc_log) >= (1L << 18));
     const int rows_per_wg = 4 * (kWave >> (lc_log + le_log));
-    const int grid = ceil_div(M, rows_per_wg);
+    const int nblocks = ceil_div(M, rows_per_wg);
+    const int grid = slices == 1 ? nblocks : ceil_div(nblocks, 8 / slices) * 8;
     const int long_len = std::max(8 << le_log << (unroll == 4 ? 2 : 1),
                                   static_cast<int>(std::ceil(std::min(4.0 * avg, 1.0e9))));
-    RowGroupArgs args{A.row_ptr, A.col_idx,  A.values, B,       C,
-                      M,         N,          A.num_cols, lc_log, le_log,
-                      long_len};
+    RowGroupArgs args{A.row_ptr, A.col_idx,  A.values,   B,          C,
+                      M,         N,          A.num_cols, lc_log,     le_log,
+                      long_len,  slices,     slice_cols, nblocks};
     hipError_t e;
     if (vec == 4) e = run_row_groups<4>(args, coop, unroll, grid, stream);
     else if (vec == 2) e = run_row_groups<2>(args, coop, unroll, grid, stream);
@@ -1062,14 +1099,16 @@ bool row_groups_pay(int M, int N, int K, double avg_row, int max_row) {
     // 300 entries, M = 2048 .. 65536): row groups win 1.5 - 4x for N <= 32,
     // 1.1 - 1.9x for N = 64, at N = 128 on matrices of >= 16384 rows
     // (1.04 - 1.3x) or rows of <= 16 entries, and at N = 256 on rows of <= 8
-    // entries.  A row longer than 4096 / column-lanes entries would keep one
+    // entries, or of <= 24 when B needs column slices (1.1 - 1.5x).  A row longer than 4096 / column-lanes entries would keep one
     // wave busy for more than 16 iterations of its wave-wide pass: then the
     // engine, which shares long rows between waves, is the safer choice.
     if (N <= 0 || M <= 0 || !b_fits_buffer(K, N)) return false;
-    const int vec = N % 4 == 0 ? 4 : (N % 2 == 0 ? 2 : 1);
-    const int lc  = 1 << row_group_lc_log(M, N, vec);
+    const int vec    = N % 4 == 0 ? 4 : (N % 2 == 0 ? 2 : 1);
+    const int slices = row_group_slices(K, N, avg_row);
+    const int lc     = 1 << row_group_lc_log(M, ceil_div(ceil_div(N, slices), vec) * vec, vec);
     if (max_row > 4096 / lc) return false;
-    return N <= 64 || (N <= 128 && M >= 16384) || N * avg_row <= 2048.0;
+    return N <= 64 || (N <= 128 && M >= 16384) || (N <= 256 && slices > 1) ||
+           N * avg_row <= 2048.0;
 }
 
 Error launch_csr_split(const CSR& A, const float* B, float* C, int N, hipStream_t stream,

@@ -286,6 +286,19 @@ def test_row_groups(S, torch, edge_cases, form, vec, entry_lanes, unroll):
         check_csr(_run_opts(S, torch, A, B, opts), C64, absC)
 
 
+@pytest.mark.parametrize("slices", [2, 4, 8])
+def test_row_groups_column_slices(S, torch, edge_cases, slices):
+    # XCD-tied column slices: each workgroup computes 1/slices of the columns
+    # (slices wider than N leave the later workgroups without columns)
+    for form in (2, 3):
+        opts = S.EngineOptsT(0, 0, 0, 0, 0, slices, 0, form, 0)
+        for name, (A, B, C64, absC) in edge_cases.items():
+            if B.shape[1] * 4 > 16383:
+                continue
+            say(f"csr row groups slices={slices} form={form} case={name}")
+            check_csr(_run_opts(S, torch, A, B, opts), C64, absC)
+
+
 @pytest.mark.parametrize("form", [2, 3])
 @pytest.mark.parametrize("entry_lanes,unroll", [(8, 2), (2, 4), (16, 4)])
 def test_row_groups_long_row_boundary(S, O, torch, form, entry_lanes, unroll):

@@ -5,8 +5,8 @@
 // enum, plan struct, function names, default arguments and reason strings.
 // The rule is the reference's (spmm_hybrid.cu:32-56): matrix cores iff
 // N % 16 == 0 && N > 0 && fill_in <= threshold.  The default threshold is the
-// MI355X crossover (kHybridDefaultThreshold below), measured by timing both
-// back ends over a fill-in sweep.
+// MI355X crossover for the given N (hybrid_default_threshold below), measured
+// by timing both back ends over a fill-in sweep.
 
 #include "csr.h"
 
@@ -26,21 +26,30 @@ struct HybridPlan {
     const char* reason    = "";
 };
 
-// Fill-in at or below which the MFMA path wins on MI355X.  Timing both back
-// ends (spmm_tiled_v3 and spmm_wmma kernels, warm) on 61 inputs -- uniform
-// random 4096^2 .. 16384^2 at fill 10 .. 50, random and banded partially
-// filled blocks at fill 10 .. 45, the five BASELINE configs -- at N = 128 and
-// 256: any cut-off in 26 .. 32 loses 5.2% on average to the faster back end
-// (59 us in total); 18 loses 15.5% (394 us), 45 loses 3.2% but 208 us, most
-// of it on large uniform inputs at fill 33 - 50, where the CSR engine is up
-// to 2x faster.  The remaining misses are uniform inputs at fill 25 - 33,
-// within 15% either way, and partially filled blocks at fill 45, where the
-// MFMA kernel is 1.1 - 1.5x faster.  The reference's 2.0 was the crossover of
-// a T4, whose tensor cores are far less ahead of its CUDA cores.
+// Fill-in at or below which the MFMA path wins on MI355X for a B of N
+// columns.  Timing both back ends as spmm_hybrid_run runs them (the CSR side
+// is the engine, its merge-path form or the sub-wave row groups, by the same
+// rule) on 33 inputs per N -- uniform random 4096^2 .. 16384^2 at fill
+// 10 .. 50, random and banded partially filled blocks at fill 10 .. 45, the
+// five BASELINE matrices -- the cut-off that loses least to the faster back
+// end is 6 - 8 at N = 16 (0.6% on average), 10 - 14 at N = 32 (2.2%), 16 - 18
+// at N = 64 (1.4%), 22 - 24 at N = 128 (1.8%) and 26 - 32 at N = 256 (0.0%).
+// Narrow B favours the CSR side: its row groups keep every lane busy there,
+// while a 16x16 block costs the MFMA kernel the same whatever N is.  A single
+// cut-off of 32 would lose 28% on average at N = 16.  The reference's 2.0 was
+// the crossover of a T4, whose tensor cores are far less ahead of its CUDA
+// cores.
+float hybrid_default_threshold(int N);
+
+// The cut-off for wide B (N >= 256), hybrid_default_threshold's largest value.
 constexpr float kHybridDefaultThreshold = 32.0f;
 
+// Default argument of hybrid_choose: any negative threshold selects
+// hybrid_default_threshold(N); the plan records the value used.
+constexpr float kHybridAutoThreshold = -1.0f;
+
 HybridPlan hybrid_choose(const CSR& h_A, int N,
-                         float fill_in_threshold = kHybridDefaultThreshold);
+                         float fill_in_threshold = kHybridAutoThreshold);
 
 // "csr" / "wmma" (spmm_hybrid.cu:28-30).
 const char* backend_name(Backend b);

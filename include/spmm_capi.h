@@ -220,7 +220,11 @@ int spmm_c_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B_fp16, float* d
                      const spmm_bsr_opts_t* opts, void* stream);
 
 /* ---- hybrid dispatch (spmm_hybrid.h:48-64) ---------------------------- */
+/* The wide-B cut-off (N >= 256) and the per-N MI355X crossover; no
+ * counterpart in the reference (its default is the constant 2.0). */
 float spmm_c_hybrid_default_threshold(void);
+float spmm_c_hybrid_default_threshold_for(int N);
+/* fill_in_threshold < 0 selects spmm_c_hybrid_default_threshold_for(N). */
 int spmm_c_hybrid_choose(const spmm_csr_t* h_A, int N, float fill_in_threshold,
                          spmm_hybrid_plan_t* out);               /* spmm_hybrid.h:48 */
 const char* spmm_c_backend_name(int backend);                    /* spmm_hybrid.h:51 */

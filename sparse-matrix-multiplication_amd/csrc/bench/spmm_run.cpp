@@ -27,7 +27,7 @@ struct Args {
     int   n = 256;
     int   warmup = 3;
     int   iters = 10;
-    float threshold = spmm::kHybridDefaultThreshold;
+    float threshold = spmm::kHybridAutoThreshold;  // per-N MI355X crossover
     bool  verify = true;
     bool  unified = false;
     int   cpu_threads = 0;
@@ -43,7 +43,8 @@ void print_usage(const char* prog) {
                  "  --seed INT       RNG seed                   (default 42)\n"
                  "  --warmup INT     warmup iterations          (default 3)\n"
                  "  --iters INT      timed iterations           (default 10)\n"
-                 "  --threshold FLT  BSR fill-in cut-off for the MFMA path (default %.2f)\n"
+                 "  --threshold FLT  BSR fill-in cut-off for the MFMA path (default: the MI355X\n"
+                 "                   crossover for N, 8 at N <= 16 .. %.0f at N >= 256)\n"
                  "  --bin PATH       load CSR from a binary file (overrides --m/--k/--density)\n"
                  "  --no-verify      skip the host fp64 correctness check\n"
                  "  --unified        single-GPU unified-memory path (CSR engine)\n"

@@ -646,6 +646,7 @@ int spmm_c_launch_repeat_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B1
 // ---- hybrid ------------------------------------------------------------------
 
 float spmm_c_hybrid_default_threshold(void) { return spmm::kHybridDefaultThreshold; }
+float spmm_c_hybrid_default_threshold_for(int N) { return spmm::hybrid_default_threshold(N); }
 
 int spmm_c_hybrid_choose(const spmm_csr_t* h_A, int N, float thr, spmm_hybrid_plan_t* out) {
     if (h_A == nullptr || out == nullptr) return set_error(SPMM_INVALID, "null argument");

@@ -1099,14 +1099,18 @@ bool row_groups_pay(int M, int N, int K, double avg_row, int max_row) {
     // 300 entries, M = 2048 .. 65536): row groups win 1.5 - 4x for N <= 32,
     // 1.1 - 1.9x for N = 64, at N = 128 on matrices of >= 16384 rows
     // (1.04 - 1.3x) or rows of <= 16 entries, and at N = 256 on rows of <= 8
-    // entries, or of <= 24 when B needs column slices (1.1 - 1.5x).  A row longer than 4096 / column-lanes entries would keep one
-    // wave busy for more than 16 iterations of its wave-wide pass: then the
-    // engine, which shares long rows between waves, is the safer choice.
+    // entries, or of <= 24 when B needs column slices (1.1 - 1.5x).  A row
+    // longer than both 4096 / column-lanes entries and 8x the average row
+    // would keep one wave busy far longer than the rest: then the engine,
+    // which shares long rows between waves, is the safer choice.
     if (N <= 0 || M <= 0 || !b_fits_buffer(K, N)) return false;
     const int vec    = N % 4 == 0 ? 4 : (N % 2 == 0 ? 2 : 1);
     const int slices = row_group_slices(K, N, avg_row);
     const int lc     = 1 << row_group_lc_log(M, ceil_div(ceil_div(N, slices), vec) * vec, vec);
-    if (max_row > 4096 / lc) return false;
+    // Skew, not length, is what row groups cannot share: rows of up to 8x the
+    // average stay in their groups or take the wave-wide pass without holding
+    // up the rest of the grid.
+    if (max_row > std::max(4096.0 / lc, 8.0 * avg_row)) return false;
     return N <= 64 || (N <= 128 && M >= 16384) || (N <= 256 && slices > 1) ||
            N * avg_row <= 2048.0;
 }

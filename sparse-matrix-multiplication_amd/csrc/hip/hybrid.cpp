@@ -16,7 +16,16 @@ namespace spmm {
 
 const char* backend_name(Backend b) { return b == Backend::TENSOR_WMMA ? "wmma" : "csr"; }
 
+float hybrid_default_threshold(int N) {
+    if (N <= 16) return 8.0f;
+    if (N <= 32) return 12.0f;
+    if (N <= 64) return 16.0f;
+    if (N <= 128) return 24.0f;
+    return kHybridDefaultThreshold;
+}
+
 HybridPlan hybrid_choose(const CSR& h_A, int N, float fill_in_threshold) {
+    if (fill_in_threshold < 0.0f) fill_in_threshold = hybrid_default_threshold(N);
     HybridPlan plan;
     plan.threshold = fill_in_threshold;
     plan.n_aligned = N > 0 && N % BSR_BLOCK == 0;

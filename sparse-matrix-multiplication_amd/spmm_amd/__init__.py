@@ -134,6 +134,7 @@ _SIGNATURES = {
     "spmm_c_wmma_opts": (_int, [_P(BsrT), _vp, _vp, _int, _P(BsrOptsT), _vp]),
     "spmm_c_launch_repeat_wmma_opts": (_int, [_P(BsrT), _vp, _vp, _int, _P(BsrOptsT), _int, _vp]),
     "spmm_c_hybrid_default_threshold": (_float, []),
+    "spmm_c_hybrid_default_threshold_for": (_float, [ctypes.c_int]),
     "spmm_c_hybrid_choose": (_int, [_P(CsrT), _int, _float, _P(HybridPlanT)]),
     "spmm_c_backend_name": (ctypes.c_char_p, [_int]),
     "spmm_c_hybrid_run": (_int, [_P(HybridPlanT), _P(CsrT), _vp, _vp, _int, _int, _int, _P(_float)]),
@@ -437,14 +438,18 @@ class Plan:
         return lib().spmm_c_backend_name(self.backend).decode()
 
 
-def hybrid_default_threshold() -> float:
-    return float(lib().spmm_c_hybrid_default_threshold())
+def hybrid_default_threshold(N: Optional[int] = None) -> float:
+    """The MI355X fill-in cut-off for a B of N columns (the wide-B value when
+    N is not given)."""
+    if N is None:
+        return float(lib().spmm_c_hybrid_default_threshold())
+    return float(lib().spmm_c_hybrid_default_threshold_for(int(N)))
 
 
 def hybrid_choose(m: HostCSR, N: int, threshold: Optional[float] = None) -> Plan:
     """Reference spmm_hybrid.cu:32-56."""
     if threshold is None:
-        threshold = hybrid_default_threshold()
+        threshold = -1.0  # the per-N MI355X crossover
     p = HybridPlanT()
     src = m.struct()
     _check(lib().spmm_c_hybrid_choose(ctypes.byref(src), N, threshold, ctypes.byref(p)))

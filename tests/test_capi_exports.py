@@ -47,6 +47,7 @@ def test_cpp_api_is_exported(S):
                 "spmm::spmm_wmma(spmm::BSR const&, __half const*, float*, int)",
                 "spmm::float_to_half(float const*, __half*, int)",
                 "spmm::hybrid_choose(spmm::CSR const&, int, float)",
+                "spmm::hybrid_default_threshold(int)",
                 "spmm::backend_name(spmm::Backend)",
                 "spmm::spmm_hybrid_run(spmm::HybridPlan const&, spmm::CSR const&, float const*, "
                 "float*, int, int, int)"):

@@ -77,3 +77,39 @@ def test_hybrid_forced_backends_agree(S, O):
     C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=16)
     check_csr(C1, C64, absC)
     check_csr(C2, C64, absC)
+
+
+NARROW_CASES = {
+    # (generator, N, expected back end): clear-cut cases of the per-N cut-off
+    "banded_n32": (lambda S: S.generate_banded_csr(8192, 8192, 64, 1003), 32, "wmma"),
+    "uniform_fill20_n16": (lambda S: S.generate_uniform_random_csr(8192, 8192, 0.05, 42), 16,
+                           "csr"),
+    "uniform_fill33_n32": (lambda S: S.generate_uniform_random_csr(8192, 8192, 0.03, 42), 32,
+                           "csr"),
+}
+
+
+@pytest.mark.parametrize("case", sorted(NARROW_CASES))
+def test_hybrid_narrow_b(S, O, case):
+    # the per-N cut-off at narrow B: the plan names the back end that is
+    # faster there (margins of 1.7x or more), runs it through spmm_hybrid_run
+    # (row groups on the CSR side) and is faster than the forced other one
+    gen, N, want = NARROW_CASES[case]
+    A = gen(S)
+    A.values = S.round_to_fp16(A.values)
+    B = S.round_to_fp16(np.random.default_rng(N).uniform(-1, 1, (A.num_cols, N))
+                        .astype(np.float32))
+    plan = S.hybrid_choose(A, N)
+    other = S.hybrid_choose(A, N, threshold=(0.5 if want == "wmma" else 1e9))
+    print(f"hybrid narrow case={case} N={N} fill={plan.fill_in_ratio:.2f} "
+          f"threshold={plan.threshold} plan={plan.backend_name}", flush=True)
+    assert plan.backend_name == want and other.backend_name != want
+    C, ms = S.hybrid_run(plan, A, B, warmup=3, iters=30)
+    _, ms_other = S.hybrid_run(other, A, B, warmup=3, iters=30)
+    print(f"  ms={ms:.4f} other_ms={ms_other:.4f}", flush=True)
+    assert ms < ms_other
+    C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=16)
+    if want == "csr":
+        check_csr(C, C64, absC)
+    else:
+        check_csr(C, C64, absC, tol=1e-5)

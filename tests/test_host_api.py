@@ -187,10 +187,17 @@ def test_hybrid_choose_matches_oracle_rule(S, O):
             assert p.n_aligned == (N > 0 and N % 16 == 0)
             assert p.fill_in_ratio == pytest.approx(fill)
     assert S.backend_name(0) == "csr" and S.backend_name(1) == "wmma"
-    # the MI355X crossover: fill 32 (this matrix has fill ~6.6 -> matrix cores)
+    # the MI355X crossover by width of B: 8 (N <= 16) .. 32 (N >= 256); this
+    # matrix has fill ~6.6 -> matrix cores at every N, and an explicit
+    # threshold keeps the reference's rule
     assert S.hybrid_default_threshold() == 32.0
-    p = S.hybrid_choose(A, 128)
-    assert p.threshold == 32.0 and p.backend_name == "wmma"
+    for N, thr in ((16, 8.0), (32, 12.0), (48, 16.0), (64, 16.0), (128, 24.0), (256, 32.0),
+                   (1024, 32.0)):
+        assert S.hybrid_default_threshold(N) == thr
+        p = S.hybrid_choose(A, N)
+        assert p.threshold == thr and p.backend_name == "wmma"
+    p = S.hybrid_choose(A, 128, 5.0)
+    assert p.threshold == 5.0 and p.backend_name == "csr"
 
 
 def test_nnz_balanced_bounds_equals_oracle(S, O):

@@ -101,6 +101,8 @@ typedef struct spmm_engine_opts_t {
                            N <= 8 (at most two 16-byte column lanes) take the
                            row groups */
     int entry_lanes;    /* row groups: entry lanes per row, power of two <= 64 */
+    int max_row_hint;   /* row groups: longest row's entries if known (0 = unknown);
+                           lets the kernel drop its long-row pass when no row needs it */
 } spmm_engine_opts_t;
 
 /* BSR matrix-core kernel tuning (0 = automatic).  No counterpart in the

@@ -153,6 +153,7 @@ spmm::engine::EngineOpts opts_from_c(const spmm_engine_opts_t* o) {
         e.global_loads   = o->global_loads;
         e.row_groups     = o->row_groups;
         e.entry_lanes    = o->entry_lanes;
+        e.max_row_hint   = o->max_row_hint;
     }
     return e;
 }

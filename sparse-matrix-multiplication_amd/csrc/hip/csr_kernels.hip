@@ -509,9 +509,9 @@ __global__ __launch_bounds__(256) void csr_split_fixup(const int* __restrict__ r
 // lanes take the row's entries e, e + LE, e + 2*LE, ... so each lane gathers
 // whole VEC-float segments of B rows for its own entries.  A wave holds
 // 64 / L rows, a 256-thread workgroup four waves; rows never cross groups, so
-// there is no row bookkeeping in the loop, no LDS and no barrier.  At the end
-// of a row the entry lanes' partials are summed with xor shuffles (fixed
-// order) and entry lane 0 stores the row.
+// there is no row bookkeeping in the loop, and the group phase needs no LDS
+// and no barrier.  At the end of a row the entry lanes' partials are summed
+// with xor shuffles (fixed order) and entry lane 0 stores the row.
 //
 // For N of a few columns the row-block engine leaves most lanes idle (its
 // groups cover columns, at most 8 per wave) and pays its per-step row tests on
@@ -521,10 +521,10 @@ __global__ __launch_bounds__(256) void csr_split_fixup(const int* __restrict__ r
 // of a few entries.
 //
 // A row longer than 8 iterations of its group (8 * LE * U entries) and than
-// 4x the average row is not taken by the group but by the whole wave
-// afterwards (64 / LC entry lanes), so one long row delays only its own wave
-// and is taken by 64 / L times the lanes.  (Rows of about average length stay
-// in their groups: moving them would only serialise the wave's rows.)  Rows far longer than that belong
+// 4x the average row is not taken by the group but by the whole workgroup
+// afterwards (4 * 64 / LC entry lanes, partials added through LDS), so it is
+// taken by 256 / L times the lanes.  (Rows of about average length stay in
+// their groups: moving them would only serialise the workgroup's rows.)  Rows far longer than that belong
 // to the engine or the merge-path partition, which share a row between waves
 // and workgroups; the dispatch rule below keeps them there.
 // ---------------------------------------------------------------------------
@@ -591,11 +591,11 @@ __device__ __forceinline__ typename Vec<VEC>::T row_segment_sum(
 template <int VEC, int U>
 __device__ __forceinline__ typename Vec<VEC>::T row_chunks_sum(
     const RowGroupArgs& a, __amdgpu_buffer_rsrc_t rb, int p0, int p1, int g0, int gl, int e,
-    int L, int LE, int colb) {
+    int L, int LE, int colb, int chunk_stride) {
     using VT = typename Vec<VEC>::T;
     VT acc = vzero<VEC>();
     const int sub = L / LE;  // sub-steps per chunk (= column lanes)
-    for (int base = p0; base < p1; base += L) {
+    for (int base = p0; base < p1; base += chunk_stride) {
         const int   q   = base + gl;
         const int   kc  = q < p1 ? a.col_idx[q] : -1;
         const float vc  = q < p1 ? a.vals[q] : 0.0f;
@@ -623,7 +623,7 @@ __device__ __forceinline__ typename Vec<VEC>::T row_chunks_sum(
     return acc;
 }
 
-template <int VEC, int U, bool COOP>
+template <int VEC, int U, bool COOP, bool LONG_ROWS>
 __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
     using VT = typename Vec<VEC>::T;
     const int LC   = 1 << a.lc_log;
@@ -644,7 +644,7 @@ __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
         rblk  = (blockIdx.x >> 3) * per + x % per;
         slice = x / per;
     }
-    if (rblk >= a.nblocks) return;  // whole workgroup; no barrier or shuffle follows it
+    if (rblk >= a.nblocks) return;  // whole workgroup, before any barrier
     const int cbeg = slice * a.slice_cols;
     const int cend = min(a.N, cbeg + a.slice_cols);
     const int row  = (rblk * 4 + wave) * (kWave / L) + (lane >> (a.lc_log + a.le_log));
@@ -654,7 +654,8 @@ __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
         start = a.row_ptr[row];
         end   = a.row_ptr[row + 1];
     }
-    const bool is_long = end - start > a.long_len;
+    // LONG_ROWS = false: the caller knows no row exceeds long_len.
+    const bool is_long = LONG_ROWS && end - start > a.long_len;
     const int  g_end   = is_long ? start : end;
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(a.B), static_cast<short>(a.N * 4), a.K, kBufWord3);
@@ -665,7 +666,7 @@ __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
         VT acc;
         if constexpr (COOP) {
             acc = row_chunks_sum<VEC, U>(a, rb, start, g_end, lane & ~(L - 1), gl, e, L, LE,
-                                         col ? n * 4 : 0);
+                                         col ? n * 4 : 0, L);
         } else {
             acc = row_segment_sum<VEC, U>(a, rb, start + e, g_end, LE, col ? n * 4 : 0);
         }
@@ -675,27 +676,48 @@ __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
         }
     }
 
-    // Long rows of this wave, one at a time with all 64 lanes.
-    unsigned long long longs = __ballot(live && is_long && gl == 0);
+    if constexpr (!LONG_ROWS) return;
+    // Long rows of this workgroup, one at a time with all four waves: wave w
+    // takes the entries of lanes w*WE .. w*WE+WE-1 of every 4*WE (per-lane
+    // loads) or every fourth 64-entry chunk (cooperative loads), and wave 0
+    // adds the four waves' partials in wave order (deterministic).
+    __shared__ int s_long_rows[4][kWave];
+    __shared__ int s_long_cnt[4];
+    __shared__ VT  s_part[4][kWave];
+    const unsigned long long longs = __ballot(live && is_long && gl == 0);
+    if (lane == 0) s_long_cnt[wave] = __popcll(longs);
+    if (live && is_long && gl == 0) {
+        s_long_rows[wave][__popcll(longs & ((1ull << lane) - 1))] = row;
+    }
+    __syncthreads();
+    const int WE = kWave / LC;  // entry lanes per wave
     const int we = lane >> a.lc_log;
-    while (longs != 0) {
-        const int src = __builtin_ctzll(longs);
-        longs &= longs - 1;
-        const int r  = __shfl(row, src);
-        const int rs = __shfl(start, src);
-        const int re = __shfl(end, src);
-        for (int n0 = cbeg; n0 < cend; n0 += LC * VEC) {
-            const int  n   = n0 + c * VEC;
-            const bool col = n < cend;
-            VT acc;
-            if constexpr (COOP) {
-                acc = row_chunks_sum<VEC, U>(a, rb, rs, re, 0, lane, we, kWave, kWave / LC,
-                                             col ? n * 4 : 0);
-            } else {
-                acc = row_segment_sum<VEC, U>(a, rb, rs + we, re, kWave / LC, col ? n * 4 : 0);
+    for (int w2 = 0; w2 < 4; ++w2) {
+        const int cnt = s_long_cnt[w2];
+        for (int i = 0; i < cnt; ++i) {
+            const int r  = s_long_rows[w2][i];
+            const int rs = a.row_ptr[r];
+            const int re = a.row_ptr[r + 1];
+            for (int n0 = cbeg; n0 < cend; n0 += LC * VEC) {
+                const int  n   = n0 + c * VEC;
+                const bool col = n < cend;
+                VT acc;
+                if constexpr (COOP) {
+                    acc = row_chunks_sum<VEC, U>(a, rb, rs + wave * kWave, re, 0, lane, we, kWave,
+                                                 WE, col ? n * 4 : 0, 4 * kWave);
+                } else {
+                    acc = row_segment_sum<VEC, U>(a, rb, rs + wave * WE + we, re, 4 * WE,
+                                                  col ? n * 4 : 0);
+                }
+                for (int m = LC; m < kWave; m <<= 1) acc = xor_add<VEC>(acc, m);
+                if (we == 0) s_part[wave][c] = acc;
+                __syncthreads();
+                if (wave == 0 && we == 0 && col) {
+                    const VT sum = ((s_part[0][c] + s_part[1][c]) + s_part[2][c]) + s_part[3][c];
+                    store_vec<VEC>(a.C + static_cast<size_t>(r) * a.N + n, sum);
+                }
+                __syncthreads();
             }
-            for (int m = LC; m < kWave; m <<= 1) acc = xor_add<VEC>(acc, m);
-            if (we == 0 && col) store_vec<VEC>(a.C + static_cast<size_t>(r) * a.N + n, acc);
         }
     }
 }
@@ -842,21 +864,27 @@ int row_group_slices(int K, int N, double avg_row) {
     return s;
 }
 
-template <int VEC, bool COOP>
+template <int VEC, bool COOP, bool LONG_ROWS>
 hipError_t run_row_groups(const RowGroupArgs& args, int unroll, int grid, hipStream_t stream) {
     if (unroll == 4) {
-        hipLaunchKernelGGL((csr_row_groups<VEC, 4, COOP>), dim3(grid), dim3(256), 0, stream, args);
+        hipLaunchKernelGGL((csr_row_groups<VEC, 4, COOP, LONG_ROWS>), dim3(grid), dim3(256), 0,
+                           stream, args);
     } else {
-        hipLaunchKernelGGL((csr_row_groups<VEC, 2, COOP>), dim3(grid), dim3(256), 0, stream, args);
+        hipLaunchKernelGGL((csr_row_groups<VEC, 2, COOP, LONG_ROWS>), dim3(grid), dim3(256), 0,
+                           stream, args);
     }
     return hipGetLastError();
 }
 
 template <int VEC>
-hipError_t run_row_groups(const RowGroupArgs& args, bool coop, int unroll, int grid,
-                          hipStream_t stream) {
-    return coop ? run_row_groups<VEC, true>(args, unroll, grid, stream)
-                : run_row_groups<VEC, false>(args, unroll, grid, stream);
+hipError_t run_row_groups(const RowGroupArgs& args, bool coop, bool long_rows, int unroll,
+                          int grid, hipStream_t stream) {
+    if (long_rows) {
+        return coop ? run_row_groups<VEC, true, true>(args, unroll, grid, stream)
+                    : run_row_groups<VEC, false, true>(args, unroll, grid, stream);
+    }
+    return coop ? run_row_groups<VEC, true, false>(args, unroll, grid, stream)
+                : run_row_groups<VEC, false, false>(args, unroll, grid, stream);
 }
 
 // Shape of the sub-wave row groups, measured on MI355X over uniform rows of
@@ -920,10 +948,13 @@ Error launch_row_groups(const CSR& A, const float* B, float* C, int N, hipStream
     RowGroupArgs args{A.row_ptr, A.col_idx,  A.values,   B,          C,
                       M,         N,          A.num_cols, lc_log,     le_log,
                       long_len,  slices,     slice_cols, nblocks};
+    // Without a longest-row hint any row may be long: the workgroup-wide pass
+    // (one barrier even when no row needs it) is compiled in.
+    const bool long_rows = o.max_row_hint <= 0 || o.max_row_hint > long_len;
     hipError_t e;
-    if (vec == 4) e = run_row_groups<4>(args, coop, unroll, grid, stream);
-    else if (vec == 2) e = run_row_groups<2>(args, coop, unroll, grid, stream);
-    else e = run_row_groups<1>(args, coop, unroll, grid, stream);
+    if (vec == 4) e = run_row_groups<4>(args, coop, long_rows, unroll, grid, stream);
+    else if (vec == 2) e = run_row_groups<2>(args, coop, long_rows, unroll, grid, stream);
+    else e = run_row_groups<1>(args, coop, long_rows, unroll, grid, stream);
     return from_hip(e, "csr row groups launch");
 }
 
@@ -1100,9 +1131,11 @@ bool row_groups_pay(int M, int N, int K, double avg_row, int max_row) {
     // 1.1 - 1.9x for N = 64, at N = 128 on matrices of >= 16384 rows
     // (1.04 - 1.3x) or rows of <= 16 entries, and at N = 256 on rows of <= 8
     // entries, or of <= 24 when B needs column slices (1.1 - 1.5x).  A row
-    // longer than both 4096 / column-lanes entries and 8x the average row
-    // would keep one wave busy far longer than the rest: then the engine,
-    // which shares long rows between waves, is the safer choice.
+    // longer than both 16384 / column-lanes entries and 8x the average row
+    // would keep one workgroup busy far longer than the rest (more than ~16
+    // iterations of its workgroup-wide pass): then the engine, which shares
+    // long rows between eight waves with more entries per step, is the safer
+    // choice.
     if (N <= 0 || M <= 0 || !b_fits_buffer(K, N)) return false;
     const int vec    = N % 4 == 0 ? 4 : (N % 2 == 0 ? 2 : 1);
     const int slices = row_group_slices(K, N, avg_row);
@@ -1110,7 +1143,7 @@ bool row_groups_pay(int M, int N, int K, double avg_row, int max_row) {
     // Skew, not length, is what row groups cannot share: rows of up to 8x the
     // average stay in their groups or take the wave-wide pass without holding
     // up the rest of the grid.
-    if (max_row > std::max(4096.0 / lc, 8.0 * avg_row)) return false;
+    if (max_row > std::max(16384.0 / lc, 8.0 * avg_row)) return false;
     return N <= 64 || (N <= 128 && M >= 16384) || (N <= 256 && slices > 1) ||
            N * avg_row <= 2048.0;
 }

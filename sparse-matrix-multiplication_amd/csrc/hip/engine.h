@@ -52,6 +52,11 @@ struct EngineOpts {
     // lanes (N <= 8 with 16-byte lanes) take the row groups.
     int row_groups     = 0;
     int entry_lanes    = 0;  // row groups: entry lanes per row, a power of two up to 64
+    // Row groups: the longest row's entries when the caller knows it (0 =
+    // unknown).  With no row longer than the long-row cut, the kernel is built
+    // without its workgroup-wide pass.  A hint below the true longest row
+    // gives wrong results for the longer rows.
+    int max_row_hint   = 0;
 };
 
 struct Error {

@@ -173,7 +173,8 @@ Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float
         if (h_A.nnz > 0 && row_groups_pay(M, N, h_A.num_cols, avg_row, max_row)) {
             // Narrow B or short rows without long ones: sub-wave row groups.
             EngineOpts rg;
-            rg.row_groups = 1;
+            rg.row_groups   = 1;
+            rg.max_row_hint = max_row;
             SPMM_TRY(time_median_launch(
                 [&] {
                     return launch_csr(CsrRole::TiledV3, csr.view, d_B.as<float>(),

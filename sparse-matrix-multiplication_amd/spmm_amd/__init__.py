@@ -68,7 +68,8 @@ class EngineOptsT(ctypes.Structure):
     _fields_ = [("vec", ctypes.c_int), ("waves", ctypes.c_int), ("unroll", ctypes.c_int),
                 ("rows_per_block", ctypes.c_int), ("groups", ctypes.c_int),
                 ("slices", ctypes.c_int), ("global_loads", ctypes.c_int),
-                ("row_groups", ctypes.c_int), ("entry_lanes", ctypes.c_int)]
+                ("row_groups", ctypes.c_int), ("entry_lanes", ctypes.c_int),
+                ("max_row_hint", ctypes.c_int)]
 
 
 class BsrOptsT(ctypes.Structure):

@@ -286,6 +286,19 @@ def test_row_groups(S, torch, edge_cases, form, vec, entry_lanes, unroll):
         check_csr(_run_opts(S, torch, A, B, opts), C64, absC)
 
 
+@pytest.mark.parametrize("form", [1, 2, 3])
+def test_row_groups_max_row_hint(S, torch, edge_cases, form):
+    # with the true longest row as a hint the kernel drops its long-row pass
+    # whenever no row needs it (and keeps it otherwise); results are the same
+    for name, (A, B, C64, absC) in edge_cases.items():
+        if B.shape[1] * 4 > 16383:
+            continue
+        hint = int(np.diff(A.row_ptr).max()) if A.num_rows else 0
+        say(f"csr row groups max_row_hint={hint} form={form} case={name}")
+        opts = S.EngineOptsT(0, 0, 0, 0, 0, 0, 0, form, 0, max(hint, 1))
+        check_csr(_run_opts(S, torch, A, B, opts), C64, absC)
+
+
 @pytest.mark.parametrize("slices", [2, 4, 8])
 def test_row_groups_column_slices(S, torch, edge_cases, slices):
     # XCD-tied column slices: each workgroup computes 1/slices of the columns

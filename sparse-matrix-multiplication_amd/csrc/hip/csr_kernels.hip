@@ -539,7 +539,7 @@ struct RowGroupArgs {
     int          K;
     int          lc_log;    // column lanes per row: 1 << lc_log
     int          le_log;    // entry lanes per row: 1 << le_log
-    int          long_len;  // rows with more entries go to the wave-wide pass
+    int          long_len;  // rows with more entries go to the workgroup-wide pass
     int          slices;    // XCD-tied column slices: 1, 2, 4 or 8
     int          slice_cols;
     int          nblocks;   // row blocks (workgroups of one column slice)
@@ -1018,9 +1018,9 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
     // Default launches of the production roles at N of a few columns (at most
     // two column lanes of VEC floats, e.g. N <= 8 with 16-byte lanes) take the
     // sub-wave row groups: the engine keeps 3/4 or more of its lanes idle
-    // there, and with 32 or 64 entry lanes the row groups' wave-wide pass still
-    // shares a long row among many lanes (measured on MI355X: 1.6 - 3.4x
-    // faster on uniform rows, 1.5 - 3x on power-law rows of up to 4096
+    // there, and with 128 or 256 entry lanes the row groups' workgroup-wide
+    // pass shares a long row among many lanes (measured on MI355X: 1.6 - 3.4x
+    // faster on uniform rows, 2.5 - 3.6x on power-law rows of up to 4096
     // entries).  Any explicit engine option keeps the engine.
     const bool engine_defaults = o.vec == 0 && o.waves == 0 && o.unroll == 0 &&
                                  o.rows_per_block == 0 && o.groups == 0 && o.slices == 0 &&
@@ -1141,7 +1141,7 @@ bool row_groups_pay(int M, int N, int K, double avg_row, int max_row) {
     const int slices = row_group_slices(K, N, avg_row);
     const int lc     = 1 << row_group_lc_log(M, ceil_div(ceil_div(N, slices), vec) * vec, vec);
     // Skew, not length, is what row groups cannot share: rows of up to 8x the
-    // average stay in their groups or take the wave-wide pass without holding
+    // average stay in their groups or take the workgroup-wide pass without holding
     // up the rest of the grid.
     if (max_row > std::max(16384.0 / lc, 8.0 * avg_row)) return false;
     return N <= 64 || (N <= 128 && M >= 16384) || (N <= 256 && slices > 1) ||

@@ -702,11 +702,12 @@ __global__ __launch_bounds__(256) void csr_row_groups(RowGroupArgs a) {
                 const int  n   = n0 + c * VEC;
                 const bool col = n < cend;
                 VT acc;
+                // One row at a time: four entries per lane in flight.
                 if constexpr (COOP) {
-                    acc = row_chunks_sum<VEC, U>(a, rb, rs + wave * kWave, re, 0, lane, we, kWave,
+                    acc = row_chunks_sum<VEC, 4>(a, rb, rs + wave * kWave, re, 0, lane, we, kWave,
                                                  WE, col ? n * 4 : 0, 4 * kWave);
                 } else {
-                    acc = row_segment_sum<VEC, U>(a, rb, rs + wave * WE + we, re, 4 * WE,
+                    acc = row_segment_sum<VEC, 4>(a, rb, rs + wave * WE + we, re, 4 * WE,
                                                   col ? n * 4 : 0);
                 }
                 for (int m = LC; m < kWave; m <<= 1) acc = xor_add<VEC>(acc, m);

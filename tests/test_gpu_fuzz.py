@@ -1,7 +1,7 @@
 """Seeded random parity sweep on cuda:0: random shapes, densities, row-length
 skew and engine options for the CSR engine (row partition, merge-path and the
-sub-wave row groups), and random shapes and kernel options for the MFMA BSR
-kernel, each checked against the CPU oracle with the same bars as the other
+sub-wave row groups, the latter also with their own forms, slices and longest-
+row hints), and random shapes and kernel options for the MFMA BSR kernel, each checked against the CPU oracle with the same bars as the other
 GPU tests (fp32 CSR within 1e-5 of the fp64 loop; fp16 BSR within 1e-2 of
 fp32 accumulation and within 1e-5 of the exact product of the fp16
 operands)."""
@@ -120,3 +120,51 @@ def test_mfma_random(S, O, torch, chunk):
         C = dC.cpu().numpy()
         check_bsr(C, C32, absC)
         check_csr(C, C64, absC, tol=1e-5)
+
+
+def _long_row_csr(S, rng, M, K):
+    """Mostly rows of 0-4 entries with ~3% rows of up to K entries."""
+    rows, cols = [], []
+    for r in range(M):
+        n = int(rng.integers(0, 5)) if rng.random() < 0.97 else int(rng.integers(1, K + 1))
+        if n:
+            rows.append(np.full(n, r))
+            cols.append(rng.choice(K, n, replace=False))
+    if not rows:
+        return S.csr_from_coo_host(M, K, [], [], [])
+    r = np.concatenate(rows)
+    c = np.concatenate(cols)
+    return S.csr_from_coo_host(M, K, r, c, rng.uniform(-1, 1, r.size).astype(np.float32))
+
+
+@pytest.mark.parametrize("chunk", range(2))
+def test_row_groups_random(S, O, torch, chunk):
+    # the sub-wave row groups under random shapes, skew, load forms, column
+    # slices, entry lanes, unroll and longest-row hints (exact or above the
+    # true longest row), plus the default launch (row groups for N <= 8)
+    rng = np.random.default_rng(3000 + chunk)
+    for case in range(40):
+        M = int(rng.integers(1, 1500))
+        K = int(rng.integers(1, 1500))
+        N = int(rng.choice([1, 2, 3, 4, 5, 8, 12, 16, 24, 32, 40, 64, 96, 128, 160, 256]))
+        A = _long_row_csr(S, rng, M, K) if rng.random() < 0.3 else _random_csr(S, rng, M, K)
+        B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+        mx = int(np.diff(A.row_ptr).max())
+        opts = S.EngineOptsT(int(rng.choice([0, 1, 2, 4])), 0, int(rng.choice([0, 2, 4])), 0, 0,
+                             int(rng.choice([0, 1, 2, 4, 8])), 0, int(rng.choice([1, 2, 3])),
+                             int(rng.choice([0, 1, 2, 4, 8, 16, 64])),
+                             int(rng.choice([0, mx, mx + 5])))
+        say(f"fuzz row groups chunk={chunk} case={case} M={M} K={K} N={N} nnz={A.nnz} max={mx} "
+            f"opts=({opts.vec},{opts.unroll},{opts.slices},{opts.row_groups},{opts.entry_lanes},"
+            f"{opts.max_row_hint})")
+        C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)
+        dA = S.DeviceCSR(A)
+        dB = torch.from_numpy(B).cuda()
+        dC = torch.full((M, N), float("nan"), device="cuda")
+        S.spmm_tiled_v3_opts(dA, dB, opts, dC)
+        torch.cuda.synchronize()
+        check_csr(dC.cpu().numpy(), C64, absC)
+        dC.fill_(float("nan"))
+        S.spmm_csr("tiled_v3", dA, dB, dC)
+        torch.cuda.synchronize()
+        check_csr(dC.cpu().numpy(), C64, absC)

@@ -1,7 +1,8 @@
 """Seeded random parity sweep on cuda:0: random shapes, densities, row-length
 skew and engine options for the CSR engine (row partition, merge-path and the
-sub-wave row groups, the latter also with their own forms, slices and longest-
-row hints), and random shapes and kernel options for the MFMA BSR kernel, each checked against the CPU oracle with the same bars as the other
+sub-wave row groups, the latter also with their own load forms, slices and
+longest-row hints), and random shapes and kernel options for the MFMA BSR
+kernel, each checked against the CPU oracle with the same bars as the other
 GPU tests (fp32 CSR within 1e-5 of the fp64 loop; fp16 BSR within 1e-2 of
 fp32 accumulation and within 1e-5 of the exact product of the fp16
 operands)."""

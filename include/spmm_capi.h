@@ -202,7 +202,8 @@ int spmm_c_tiled_v3_partitioned(const spmm_csr_t* d_A, const int* d_bounds, int 
 int spmm_c_default_partition_parts(int num_rows, int nnz);
 /* Merge-path partition (no counterpart in the reference; used by spmm_hybrid_run):
  * part g multiplies nonzeros [nnz*g/parts, nnz*(g+1)/parts), cutting long rows
- * between workgroups.  d_split_rows: parts+1 ints from spmm_c_nnz_split_rows;
+ * between workgroups (1 <= parts <= max(nnz, 1), else SPMM_INVALID).
+ * d_split_rows: parts+1 ints from spmm_c_nnz_split_rows;
  * d_carry: a workspace of parts * N floats.  Two launches (the engine, then
  * the carry fix-up); results are deterministic. */
 int spmm_c_nnz_split_rows(const spmm_csr_t* h, int parts, int* h_rows_out);

@@ -476,28 +476,67 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
 
 // Merge-path fix-up: row r that continues into parts g0+1 .. g1 was stored by
 // the part where it starts; the first continuation part adds the carries of
-// parts g0+1 .. g1 in part order (deterministic) to C[r].
-__global__ __launch_bounds__(256) void csr_split_fixup(const int* __restrict__ row_ptr,
-                                                       const int* __restrict__ split_rows,
-                                                       const float* __restrict__ carry,
-                                                       float* __restrict__ C, int M, int N,
-                                                       long long nnz, int parts) {
-    auto head_row = [&](int q) -> int {
-        const long long lo = nnz * q / parts;
-        const long long hi = nnz * (q + 1) / parts;
-        const int r = split_rows[q];
-        return (lo < hi && r < M && row_ptr[r] < lo) ? r : -1;
-    };
-    const int g = blockIdx.x;
-    const int r = head_row(g);
-    if (r < 0) return;
-    if (g > 0 && head_row(g - 1) == r) return;  // not the first continuation of row r
-    int last = g;
-    while (last + 1 < parts && head_row(last + 1) == r) ++last;
-    for (int c = threadIdx.x; c < N; c += blockDim.x) {
-        float s = 0.f;
-        for (int q = g; q <= last; ++q) s += carry[static_cast<size_t>(q) * N + c];
-        C[static_cast<size_t>(r) * N + c] += s;
+// parts g0+1 .. g1 in part order (deterministic) to C[r].  Every part holds at
+// least one nonzero (the launcher requires parts <= nnz), so part q > g
+// continues row r exactly when split_rows[q] == r.  One wave per part, and
+// the loads are arranged in three dependent rounds: the part's row; that
+// row's first nonzero together with the rows of the next 64 parts (a ballot
+// finds where the run ends); the carries together with C.
+constexpr int kFixupCols = 4;  // columns per lane in flight
+
+__global__ __launch_bounds__(64) void csr_split_fixup(const int* __restrict__ row_ptr,
+                                                      const int* __restrict__ split_rows,
+                                                      const float* __restrict__ carry,
+                                                      float* __restrict__ C, int M, int N,
+                                                      long long nnz, int parts) {
+    const int g    = blockIdx.x;
+    const int lane = threadIdx.x;
+    const long long lo = nnz * g / parts;
+    const long long hi = nnz * (g + 1) / parts;
+    const int r  = split_rows[g];
+    const int rp = g > 0 ? split_rows[g - 1] : -1;
+    if (!(lo < hi && r >= 0 && r < M)) return;
+    int base = g + 1;
+    int q    = base + lane;
+    int w    = q < parts ? split_rows[q] : -1;  // issued before row_ptr[r] returns
+    const int rs = row_ptr[r];
+    if (rs >= lo) return;  // part g starts row r and stored it
+    // part g continues row r; the previous part also continues it when it
+    // holds row r and r began before that part's first nonzero
+    if (g > 0 && rp == r && rs < nnz * (g - 1) / parts) return;
+    int last;
+    for (;;) {
+        const unsigned long long stop = __ballot(!(q < parts && w == r));
+        if (stop != 0ull) {
+            last = base + __ffsll(static_cast<long long>(stop)) - 2;
+            break;
+        }
+        base += 64;
+        q = base + lane;
+        w = q < parts ? split_rows[q] : -1;
+    }
+    float* crow = C + static_cast<size_t>(r) * N;
+    for (int c0 = 0; c0 < N; c0 += 64 * kFixupCols) {
+        float cv[kFixupCols], s[kFixupCols];
+#pragma unroll
+        for (int j = 0; j < kFixupCols; ++j) {
+            const int c = c0 + lane + 64 * j;
+            cv[j] = c < N ? crow[c] : 0.f;
+            s[j]  = 0.f;
+        }
+        for (int p = g; p <= last; ++p) {
+            const float* cr = carry + static_cast<size_t>(p) * N;
+#pragma unroll
+            for (int j = 0; j < kFixupCols; ++j) {
+                const int c = c0 + lane + 64 * j;
+                if (c < N) s[j] += cr[c];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kFixupCols; ++j) {
+            const int c = c0 + lane + 64 * j;
+            if (c < N) crow[c] = cv[j] + s[j];
+        }
     }
 }
 
@@ -1093,7 +1132,7 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
         e = dispatch_groups<1>(groups, waves, unroll, sbuf, args, grid, stream);
     }
     if (e == hipSuccess && split != nullptr) {
-        hipLaunchKernelGGL(csr_split_fixup, dim3(split->parts), dim3(256), 0, stream, A.row_ptr,
+        hipLaunchKernelGGL(csr_split_fixup, dim3(split->parts), dim3(64), 0, stream, A.row_ptr,
                            split->rows, split->carry, C, M, N, static_cast<long long>(A.nnz),
                            split->parts);
         e = hipGetLastError();
@@ -1153,6 +1192,12 @@ Error launch_csr_split(const CSR& A, const float* B, float* C, int N, hipStream_
                        const SplitPlan& plan, const EngineOpts* opts) {
     if (plan.parts < 1 || plan.rows == nullptr) {
         return fail(kInvalid, "split partition needs parts >= 1 and its row table");
+    }
+    if (plan.parts > std::max(A.nnz, 1)) {
+        // an empty part would break the fix-up's runs of continuation parts
+        return fail(kInvalid, "split partition needs parts <= max(nnz, 1) (got parts=" +
+                                  std::to_string(plan.parts) + ", nnz=" +
+                                  std::to_string(A.nnz) + ")");
     }
     if (plan.carry == nullptr && N > 0 && A.num_rows > 0) {
         return fail(kInvalid, "split partition needs a carry workspace of parts x N floats");

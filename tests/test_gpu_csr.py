@@ -247,6 +247,19 @@ def test_split_engine_errors(S, torch):
     s = S.CsrT(4, 4, 1, 0, 0, 0)
     assert S.lib().spmm_c_tiled_v3_split(ctypes.byref(s), None, 1, 0, 0, 4, None, None) == \
         S.SPMM_INVALID
+    # more parts than nonzeros (an empty part) is refused before any launch
+    A = S.csr_from_coo_host(4, 4, [0, 0, 1], [0, 1, 2], [1.0, 2.0, 3.0])
+    dA = S.DeviceCSR(A)
+    B = torch.ones((4, 8), device="cuda")
+    rows = torch.zeros(5, dtype=torch.int32, device="cuda")  # 4 parts > 3 nonzeros
+    with pytest.raises(S.SpmmError) as e:
+        S.spmm_tiled_v3_split(dA, rows, B)
+    assert e.value.code == S.SPMM_INVALID
+    assert "parts <= max(nnz, 1)" in str(e.value)
+    # parts == nnz is the largest accepted split
+    C = S.spmm_tiled_v3_split(dA, torch.from_numpy(S.nnz_split_rows(A, 3)).cuda(), B)
+    torch.cuda.synchronize()
+    assert np.allclose(C.cpu().numpy(), A.to_dense() @ np.ones((4, 8), np.float32))
 
 
 def test_tiled_v2_contract(S, torch, edge_cases):

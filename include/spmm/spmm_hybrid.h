@@ -59,8 +59,10 @@ const char* backend_name(Backend b);
 // `warmup` untimed and `iters` timed launches (hipEvents per launch on the null
 // stream, like spmm_hybrid.cu:87-116), copies C back and returns the median
 // per-launch time in milliseconds.  Setup is outside the timed region.
-// The CSR branch launches the engine with the host-computed nnz-balanced
-// workgroup partition (nnz_balanced_bounds), uploaded once with A.
+// The CSR branch picks from the host CSR's row lengths: sub-wave row groups
+// (narrow B, short rows, N <= 128 on >= 4096 even rows), the merge-path
+// partition (a row of more than 2560 entries, its row table and carry
+// workspace set up once), or the row-block engine given the longest row.
 float spmm_hybrid_run(const HybridPlan& plan,
                       const CSR& h_A, const float* h_B, float* h_C,
                       int N, int warmup, int iters);

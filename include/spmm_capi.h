@@ -101,8 +101,13 @@ typedef struct spmm_engine_opts_t {
                            N <= 8 (at most two 16-byte column lanes) take the
                            row groups */
     int entry_lanes;    /* row groups: entry lanes per row, power of two <= 64 */
-    int max_row_hint;   /* row groups: longest row's entries if known (0 = unknown);
-                           lets the kernel drop its long-row pass when no row needs it */
+    int max_row_hint;   /* longest row's entries if known (0 = unknown).
+                           row_groups != 0: lets the kernel drop its long-row
+                           pass when no row needs it (a hint below the true
+                           longest row gives wrong results for the longer rows).
+                           row_groups == 0: rows within 2 x average + 32 entries
+                           give the row-block engine a grid of whole rounds of
+                           4-wave workgroups; a wrong hint only costs time */
 } spmm_engine_opts_t;
 
 /* BSR matrix-core kernel tuning (0 = automatic).  No counterpart in the

@@ -852,6 +852,32 @@ int auto_slices(int K, int N) {
 
 int default_waves(int slices) { return slices == 1 ? 8 : 4; }
 
+// Waves of the engine resident at once on the chip: 16 per CU (four 4-wave
+// workgroups) on 256 CUs.
+constexpr long kRoundWaves = 4096;
+
+// Rows whose lengths stay within twice the average (plus a constant for
+// short rows): uniform random rows qualify, power-law rows do not.
+bool rows_even(int M, long long nnz, int max_row) {
+    return max_row > 0 && M > 0 &&
+           max_row <= 2.0 * static_cast<double>(nnz) / M + 32.0;
+}
+
+// Rows per workgroup of the 4-wave row-block launch for even rows: the grid
+// is a whole number of rounds of kRoundWaves waves, one round per ~2 M entry
+// visits (nnz x slices, ~512 entries per wave).  A partial last round leaves
+// CUs idle while it runs.  Measured on MI355X over uniform rows (M 2048 ..
+// 32768, 8 .. 164 entries per row, N 64 .. 256), whole rounds gain up to
+// 1.35x over ~160 entries per wave (1.2 - 1.6 rounds at M = 12288 .. 16384).
+// Skewed rows need the many small workgroups of the default instead: a
+// static one-round partition loses up to 1.5x on power-law rows.
+int round_rows_per_block(int M, long long nnz, int slices, int waves) {
+    const double visits = static_cast<double>(nnz) * slices;
+    const long rounds = std::max(1L, std::lround(visits / (kRoundWaves * 512.0)));
+    const long blocks = std::max(1L, rounds * kRoundWaves / (static_cast<long>(waves) * slices));
+    return static_cast<int>(std::min<long>(kRpCap, std::max(1L, (M + blocks - 1) / blocks)));
+}
+
 // B rows as buffer records: the record stride field holds at most 16383
 // bytes and the buffer's byte range must fit a signed 32-bit offset.
 bool b_fits_buffer(int K, int N) {
@@ -1069,7 +1095,8 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
         (role == CsrRole::TiledV3 || role == CsrRole::TiledV4) &&
         b_fits_buffer(A.num_cols, N) && pow2_log_at_least(ceil_div(N, vec)) <= 1) {
         EngineOpts rg = o;
-        rg.row_groups = 1;
+        rg.row_groups   = 1;
+        rg.max_row_hint = 0;  // with row_groups = 0 the hint only ever chooses a grid
         return launch_row_groups(A, B, C, N, stream, vec, rg);
     }
     if (o.row_groups != 0) {
@@ -1096,7 +1123,12 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
     // sliced launch has twice the workgroups per row block), 4 entries per
     // group in flight per step (two steps in flight), about 160 nonzeros per
     // wave and at least 512 workgroups (two per CU) when the matrix allows it.
+    // Rows known to be even (max_row_hint): the whole-round grid of 4-wave
+    // workgroups.
+    const bool even = split == nullptr && bounds == nullptr && o.rows_per_block <= 0 &&
+                      rows_even(M, A.nnz, o.max_row_hint);
     const int waves = (o.waves == 2 || o.waves == 4 || o.waves == 8) ? o.waves
+                      : even                                         ? 4
                                                                      : default_waves(slices);
     const int unroll = o.unroll == 8 ? 8 : 4;
     const bool sbuf = o.global_loads == 0 && b_fits_buffer(A.num_cols, N);
@@ -1113,7 +1145,9 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
         args.nblocks = parts;
     } else {
         int rpb = o.rows_per_block;
-        if (rpb <= 0) {
+        if (rpb <= 0 && even) {
+            rpb = round_rows_per_block(M, A.nnz, slices, waves);
+        } else if (rpb <= 0) {
             const double avg = A.nnz > 0 ? static_cast<double>(A.nnz) / M : 1.0;
             rpb = static_cast<int>(160.0 * waves / std::max(avg, 1.0) + 0.5);
             rpb = std::min(rpb, M / 512);
@@ -1166,26 +1200,35 @@ bool split_pays(int max_row_nnz) {
 }
 
 bool row_groups_pay(int M, int N, int K, double avg_row, int max_row) {
-    // Measured on MI355X against the row-block engine (uniform rows of 1 ..
-    // 300 entries, M = 2048 .. 65536): row groups win 1.5 - 4x for N <= 32,
-    // 1.1 - 1.9x for N = 64, at N = 128 on matrices of >= 16384 rows
-    // (1.04 - 1.3x) or rows of <= 16 entries, and at N = 256 on rows of <= 8
-    // entries, or of <= 24 when B needs column slices (1.1 - 1.5x).  A row
-    // longer than both 16384 / column-lanes entries and 8x the average row
-    // would keep one workgroup busy far longer than the rest (more than ~16
-    // iterations of its workgroup-wide pass): then the engine, which shares
-    // long rows between eight waves with more entries per step, is the safer
-    // choice.
+    // Measured on MI355X against the row-block engine as the hybrid runs it
+    // (uniform rows of 8 .. 300 entries, M = 1024 .. 32768, N = 64 .. 256,
+    // the engine with the longest row as its hint; power-law rows capped at
+    // 512 / 4096).  Row groups win 1.5 - 4x for N <= 32 and 1.1 - 1.7x for
+    // N = 64 (not on 1024 rows of > 100 entries, 0.75 - 0.9x).  Above
+    // N = 64 they win on short rows (N x average <= 4096), when B needs
+    // column slices, and at N = 128 on >= 4096 rows (1.03 - 1.6x) or >= 2048
+    // rows of up to 10600 / N entries -- except at 4097 .. 8192 rows of
+    // >= 64 entries, where the engine's whole-round grid holds 1 - 2 rows
+    // per wave and matches or beats them (0.97 - 1.00x).  Those wins need
+    // even rows: power-law rows of mean 164 capped at 512 run 0.6 - 0.7x.
+    // With this rule the mean loss to the faster form over the sweep is
+    // 0.14% (worst 5.6%).  A row longer than both 16384 / column-lanes
+    // entries and 8x the average would keep one workgroup busy far longer
+    // than the rest (more than ~16 iterations of its workgroup-wide pass):
+    // then the engine, which shares long rows between eight waves with more
+    // entries per step, is the safer choice.
     if (N <= 0 || M <= 0 || !b_fits_buffer(K, N)) return false;
     const int vec    = N % 4 == 0 ? 4 : (N % 2 == 0 ? 2 : 1);
     const int slices = row_group_slices(K, N, avg_row);
     const int lc     = 1 << row_group_lc_log(M, ceil_div(ceil_div(N, slices), vec) * vec, vec);
-    // Skew, not length, is what row groups cannot share: rows of up to 8x the
-    // average stay in their groups or take the workgroup-wide pass without holding
-    // up the rest of the grid.
     if (max_row > std::max(16384.0 / lc, 8.0 * avg_row)) return false;
-    return N <= 64 || (N <= 128 && M >= 16384) || (N <= 256 && slices > 1) ||
-           N * avg_row <= 2048.0;
+    if (N <= 64) return M >= 2048 || avg_row <= 100.0;
+    if (N * avg_row <= 2048.0 || (N <= 256 && slices > 1)) return true;
+    if (max_row > 2.0 * avg_row + 32.0) return false;  // uneven rows
+    if (N * avg_row <= 4096.0) return true;
+    if (N > 128) return false;
+    if (M > 4096 && M <= 8192 && avg_row >= 64.0) return false;
+    return M >= 4096 || (M >= 2048 && N * avg_row <= 10600.0);
 }
 
 Error launch_csr_split(const CSR& A, const float* B, float* C, int N, hipStream_t stream,

@@ -52,10 +52,14 @@ struct EngineOpts {
     // lanes (N <= 8 with 16-byte lanes) take the row groups.
     int row_groups     = 0;
     int entry_lanes    = 0;  // row groups: entry lanes per row, a power of two up to 64
-    // Row groups: the longest row's entries when the caller knows it (0 =
-    // unknown).  With no row longer than the long-row cut, the kernel is built
-    // without its workgroup-wide pass.  A hint below the true longest row
-    // gives wrong results for the longer rows.
+    // The longest row's entries when the caller knows it (0 = unknown).
+    // row_groups != 0: with no row longer than the long-row cut, the kernel
+    // is built without its workgroup-wide pass; a hint below the true longest
+    // row gives wrong results for the longer rows.  row_groups == 0 (also
+    // where N <= 8 takes the row groups by default, which then ignore it):
+    // rows within 2 x average + 32 entries give the row-block engine's
+    // implicit partition a grid of whole rounds of 4-wave workgroups instead
+    // of ~160 entries per wave; a wrong hint only costs time.
     int max_row_hint   = 0;
 };
 

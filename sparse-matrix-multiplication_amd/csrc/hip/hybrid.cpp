@@ -182,10 +182,14 @@ Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float
                 },
                 warmup, iters, ms));
         } else if (h_A.nnz == 0 || !split_pays(max_row)) {
+            // The row-block engine; the longest row lets it take the
+            // whole-round grid when rows are even.
+            EngineOpts eo;
+            eo.max_row_hint = max_row;
             SPMM_TRY(time_median_launch(
                 [&] {
                     return launch_csr(CsrRole::TiledV3, csr.view, d_B.as<float>(),
-                                      d_C.as<float>(), N, nullptr);
+                                      d_C.as<float>(), N, nullptr, nullptr, 0, &eo);
                 },
                 warmup, iters, ms));
         } else {

@@ -312,6 +312,41 @@ def test_row_groups_max_row_hint(S, torch, edge_cases, form):
         check_csr(_run_opts(S, torch, A, B, opts), C64, absC)
 
 
+@pytest.mark.parametrize("hint_kind", ["true", "average", "one"])
+def test_engine_whole_round_grid(S, O, torch, edge_cases, hint_kind):
+    # the row-block engine with a longest-row hint: rows within 2 x average +
+    # 32 take the grid of whole rounds of 4-wave workgroups (1 .. kRpCap rows
+    # per workgroup, 1 / 2 / 4 column slices); the hint only chooses the grid,
+    # so a hint below the true longest row (power-law rows, ragged edge
+    # cases) must give the same results as the true one
+    for name, (A, B, C64, absC) in edge_cases.items():
+        if A.num_rows == 0 or A.nnz == 0:
+            continue
+        lens = np.diff(A.row_ptr)
+        hint = {"true": int(lens.max()), "average": max(1, A.nnz // A.num_rows), "one": 1}[hint_kind]
+        say(f"csr engine whole-round hint={hint} ({hint_kind}) case={name}")
+        opts = S.EngineOptsT(0, 0, 0, 0, 0, 0, 0, 0, 0, hint)
+        check_csr(_run_opts(S, torch, A, B, opts), C64, absC)
+    rng = np.random.default_rng(17)
+    shapes = [(1, 300, 16, 128), (1000, 2048, 8, 64), (4096, 4096, 41, 128), (12288, 12288, 5, 128),
+              (9000, 20000, 3, 256), (70000, 4096, 2, 8)]
+    for M, K, avg, N in shapes:
+        A = S.generate_uniform_random_csr(M, K, min(1.0, avg / K), 100 + M)
+        B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+        C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)
+        lens = np.diff(A.row_ptr)
+        hint = {"true": int(lens.max()), "average": max(1, A.nnz // M), "one": 1}[hint_kind]
+        say(f"csr engine whole-round hint={hint} ({hint_kind}) M={M} K={K} N={N} nnz={A.nnz}")
+        opts = S.EngineOptsT(0, 0, 0, 0, 0, 0, 0, 0, 0, hint)
+        check_csr(_run_opts(S, torch, A, B, opts), C64, absC)
+    A = S.generate_power_law_csr(8192, 8192, 64.0, 1.5, 2048, 9)
+    B = rng.uniform(-1, 1, (8192, 128)).astype(np.float32)
+    C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)
+    hint = {"true": int(np.diff(A.row_ptr).max()), "average": A.nnz // 8192, "one": 1}[hint_kind]
+    say(f"csr engine whole-round hint={hint} ({hint_kind}) power-law nnz={A.nnz}")
+    check_csr(_run_opts(S, torch, A, B, S.EngineOptsT(0, 0, 0, 0, 0, 0, 0, 0, 0, hint)), C64, absC)
+
+
 @pytest.mark.parametrize("slices", [2, 4, 8])
 def test_row_groups_column_slices(S, torch, edge_cases, slices):
     # XCD-tied column slices: each workgroup computes 1/slices of the columns

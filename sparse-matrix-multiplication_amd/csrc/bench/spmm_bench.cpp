@@ -22,9 +22,11 @@
 #include <string>
 #include <vector>
 
+#include "../hip/engine.h"
 #include "common.h"
 #include "spmm/bsr.h"
 #include "spmm/csr.h"
+#include "spmm/partition.h"
 #include "spmm/kernels/spmm_baseline.h"
 #include "spmm/kernels/spmm_memopt.h"
 #include "spmm/kernels/spmm_memopt_v2.h"
@@ -67,8 +69,9 @@ void print_usage(const char* prog) {
                  "  --batch INT      launches per timed batch (default 50)\n"
                  "  --bin PATH       load CSR from binary file (overrides --m/--k/--density)\n"
                  "  --kernel STR     baseline | memopt | memopt_v2 | tiled | tiled_v2 | tiled_v3\n"
-                 "                   | tiled_v4 | wmma | hybrid | unified | both | all\n"
-                 "                   both = baseline + memopt (default); all = every kernel\n"
+                 "                   | tiled_v4 | csr_auto | wmma | hybrid | unified | both | all\n"
+                 "                   both = baseline + memopt (default); all = every kernel;\n"
+                 "                   csr_auto = the CSR form the hybrid picks, timed in batches\n"
                  "  --cpu-threads INT host threads of the fp64 reference (default: all)\n"
                  "  --cpu-reps INT   timed repetitions of the fp64 reference (default 3)\n"
                  "  --no-cpu-1t      skip the one-thread run of the fp64 reference\n"
@@ -230,6 +233,48 @@ int main(int argc, char** argv) {
         finish(r);
         r.bytes = drv::csr_bytes(M, K, N, h_A.nnz);
         results.push_back(r);
+    }
+
+    if (ks == "csr_auto" || ks == "all") {
+        // The CSR form spmm_hybrid_run's CSR branch picks from the row lengths
+        // (row groups, the engine with the longest row as hint, or the
+        // merge-path partition), timed like the kernels above.
+        namespace eng = spmm::engine;
+        const eng::CsrChoice ch = eng::choose_csr_form(h_A, N);
+        int* d_rows = nullptr;
+        float* d_carry = nullptr;
+        eng::SplitPlan plan;
+        if (ch.form == eng::CsrForm::Split) {
+            const std::vector<int> rows = spmm::nnz_split_rows(h_A, ch.parts);
+            HIP_CHECK(hipMalloc(&d_rows, sizeof(int) * rows.size()));
+            HIP_CHECK(hipMemcpy(d_rows, rows.data(), sizeof(int) * rows.size(),
+                                hipMemcpyHostToDevice));
+            HIP_CHECK(hipMalloc(&d_carry, sizeof(float) * static_cast<size_t>(ch.parts) * N));
+            plan.rows  = d_rows;
+            plan.parts = ch.parts;
+            plan.carry = d_carry;
+        }
+        auto launch = [&] {
+            const eng::Error e =
+                ch.form == eng::CsrForm::Split
+                    ? eng::launch_csr_split(d_A, d_B, d_C, N, nullptr, plan)
+                    : eng::launch_csr(eng::CsrRole::TiledV3, d_A, d_B, d_C, N, nullptr, nullptr,
+                                      0, &ch.opts);
+            if (e.status != eng::kOk) {
+                std::fprintf(stderr, "csr_auto launch failed: %s\n", e.message.c_str());
+                std::exit(EXIT_FAILURE);
+            }
+        };
+        Result r;
+        r.name = std::string("csr_auto[") + eng::csr_form_name(ch.form) + "]";
+        time_launches(launch, args, &r.time_ms, &r.single_ms);
+        r.cold_ms = cold(launch);
+        fetch_compare(r);
+        finish(r);
+        r.bytes = drv::csr_bytes(M, K, N, h_A.nnz);
+        results.push_back(r);
+        if (d_rows != nullptr) HIP_CHECK(hipFree(d_rows));
+        if (d_carry != nullptr) HIP_CHECK(hipFree(d_carry));
     }
 
     if (ks == "wmma" || ks == "all") {

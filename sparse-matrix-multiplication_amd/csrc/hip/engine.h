@@ -138,5 +138,20 @@ bool row_groups_pay(int M, int N, int K, double avg_row, int max_row);
 // Number of workgroups the engine uses for an explicit partition of this CSR.
 int default_partition_parts(int num_rows, int nnz);
 
+// The CSR form spmm_hybrid_run's CSR branch runs for a host CSR and a B of N
+// columns, decided from its row lengths: sub-wave row groups when
+// row_groups_pay, the merge-path partition when split_pays (parts from
+// split_partition_parts), the row-block engine otherwise.  opts carries the
+// longest row as max_row_hint (and row_groups = 1 for row groups).
+enum class CsrForm { RowGroups, Engine, Split };
+struct CsrChoice {
+    CsrForm    form    = CsrForm::Engine;
+    EngineOpts opts;
+    int        parts   = 0;  // merge-path parts (Split only)
+    int        max_row = 0;
+};
+CsrChoice choose_csr_form(const CSR& h_A, int N);
+const char* csr_form_name(CsrForm f);  // "rowgroups", "engine", "split"
+
 }  // namespace engine
 }  // namespace spmm

@@ -117,6 +117,29 @@ Error upload_bsr(const BSR_host& h, DeviceBsrCopy& d) {
 
 }  // namespace
 
+CsrChoice choose_csr_form(const CSR& h_A, int N) {
+    CsrChoice ch;
+    const int M = h_A.num_rows;
+    for (int r = 0; r < M; ++r) {
+        ch.max_row = std::max(ch.max_row, h_A.row_ptr[r + 1] - h_A.row_ptr[r]);
+    }
+    ch.opts.max_row_hint = ch.max_row;
+    if (h_A.nnz <= 0 || M <= 0) return ch;
+    const double avg_row = static_cast<double>(h_A.nnz) / M;
+    if (row_groups_pay(M, N, h_A.num_cols, avg_row, ch.max_row)) {
+        ch.form            = CsrForm::RowGroups;
+        ch.opts.row_groups = 1;
+    } else if (split_pays(ch.max_row)) {
+        ch.form  = CsrForm::Split;
+        ch.parts = split_partition_parts(h_A.nnz);
+    }
+    return ch;
+}
+
+const char* csr_form_name(CsrForm f) {
+    return f == CsrForm::RowGroups ? "rowgroups" : (f == CsrForm::Split ? "split" : "engine");
+}
+
 Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float* h_C, int N,
                  int warmup, int iters, float* ms) {
     *ms = 0.f;
@@ -163,47 +186,31 @@ Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float
         // (power-law inputs) would leave their workgroups running long after
         // the rest, so then the engine runs the merge-path partition instead:
         // equal nonzero ranges per workgroup, long rows cut between them.
-        // Narrow B (N <= 64) or rows of a few entries, with no long row, go to
-        // the sub-wave row groups, which keep every lane busy there.
+        // Narrow B, short rows and tall matrices of even rows, with no long
+        // row, go to the sub-wave row groups (row_groups_pay).
         DeviceCsrCopy csr;
         SPMM_TRY(upload_csr(h_A, csr));
-        int max_row = 0;
-        for (int r = 0; r < M; ++r) max_row = std::max(max_row, h_A.row_ptr[r + 1] - h_A.row_ptr[r]);
-        const double avg_row = static_cast<double>(h_A.nnz) / M;
-        if (h_A.nnz > 0 && row_groups_pay(M, N, h_A.num_cols, avg_row, max_row)) {
-            // Narrow B or short rows without long ones: sub-wave row groups.
-            EngineOpts rg;
-            rg.row_groups   = 1;
-            rg.max_row_hint = max_row;
+        const CsrChoice ch = choose_csr_form(h_A, N);
+        if (ch.form != CsrForm::Split) {
+            // Row groups, or the row-block engine given the longest row (the
+            // whole-round grid when rows are even).
             SPMM_TRY(time_median_launch(
                 [&] {
                     return launch_csr(CsrRole::TiledV3, csr.view, d_B.as<float>(),
-                                      d_C.as<float>(), N, nullptr, nullptr, 0, &rg);
-                },
-                warmup, iters, ms));
-        } else if (h_A.nnz == 0 || !split_pays(max_row)) {
-            // The row-block engine; the longest row lets it take the
-            // whole-round grid when rows are even.
-            EngineOpts eo;
-            eo.max_row_hint = max_row;
-            SPMM_TRY(time_median_launch(
-                [&] {
-                    return launch_csr(CsrRole::TiledV3, csr.view, d_B.as<float>(),
-                                      d_C.as<float>(), N, nullptr, nullptr, 0, &eo);
+                                      d_C.as<float>(), N, nullptr, nullptr, 0, &ch.opts);
                 },
                 warmup, iters, ms));
         } else {
-            const int parts = split_partition_parts(h_A.nnz);
-            const std::vector<int> rows = nnz_split_rows(h_A, parts);
+            const std::vector<int> rows = nnz_split_rows(h_A, ch.parts);
             DeviceBuffer d_rows, d_carry;
             SPMM_TRY_HIP(hipMalloc(&d_rows.p, sizeof(int) * rows.size()), "hipMalloc");
             SPMM_TRY_HIP(hipMemcpy(d_rows.p, rows.data(), sizeof(int) * rows.size(),
                                    hipMemcpyHostToDevice), "hipMemcpy");
-            SPMM_TRY_HIP(hipMalloc(&d_carry.p, sizeof(float) * static_cast<size_t>(parts) * N),
+            SPMM_TRY_HIP(hipMalloc(&d_carry.p, sizeof(float) * static_cast<size_t>(ch.parts) * N),
                          "hipMalloc");
             SplitPlan plan;
             plan.rows  = d_rows.as<int>();
-            plan.parts = parts;
+            plan.parts = ch.parts;
             plan.carry = d_carry.as<float>();
             SPMM_TRY(time_median_launch(
                 [&] {

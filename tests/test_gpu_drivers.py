@@ -39,8 +39,10 @@ def test_bench_all_kernels_uniform():
               "--cpu-reps", "1"])
     assert r.returncode == 0, r.stderr
     recs = {d["kernel"]: d for d in _lines(r.stdout, "kernel=")}
-    assert set(recs) == set(CSR_KERNELS) | {"wmma", "hybrid[wmma]"} or \
-        set(recs) == set(CSR_KERNELS) | {"wmma", "hybrid[csr]"}
+    # 14 entries per row at N = 128: the hybrid's CSR side is the row groups
+    assert set(recs) == set(CSR_KERNELS) | {"csr_auto[rowgroups]", "wmma", "hybrid[wmma]"} or \
+        set(recs) == set(CSR_KERNELS) | {"csr_auto[rowgroups]", "wmma", "hybrid[csr]"}
+    assert float(recs["csr_auto[rowgroups]"]["rel_l2_err"]) < 1e-6
     for k in CSR_KERNELS:
         d = recs[k]
         assert (d["m"], d["k"], d["n"]) == ("512", "700", "128")
@@ -50,6 +52,27 @@ def test_bench_all_kernels_uniform():
     # fp16 rounding of fp32 inputs: the reference's wmma sits near 2.6e-4
     assert float(recs["wmma"]["rel_l2_err"]) < 1e-2
     assert "pct_mfma" in recs["wmma"]
+
+
+@pytest.mark.parametrize("args,form", [
+    (["--m", "2048", "--k", "2048", "--n", "256", "--density", "0.05"], "engine"),
+    (["--m", "3000", "--k", "3000", "--n", "64", "--density", "0.01"], "rowgroups"),
+    (["--m", "2048", "--k", "4096", "--n", "128", "--pattern", "power-law", "--mean-deg", "200",
+      "--cap", "4096"], None),
+])
+def test_bench_csr_auto(args, form):
+    # the CSR form the hybrid picks, timed in batches: row groups, the engine
+    # with the longest row as hint, or the merge-path partition for rows
+    # longer than 2560 entries
+    r = _run([BENCH] + args + ["--kernel", "csr_auto", "--warmup", "1", "--iters", "3",
+                               "--batch", "4", "--cpu-reps", "1", "--no-cpu-1t"])
+    assert r.returncode == 0, r.stderr
+    d = _lines(r.stdout, "kernel=")[0]
+    kinds = {"csr_auto[engine]", "csr_auto[rowgroups]", "csr_auto[split]"}
+    assert d["kernel"] in kinds
+    if form is not None:
+        assert d["kernel"] == f"csr_auto[{form}]"
+    assert float(d["rel_l2_err"]) < 1e-6 and float(d["cold_ms"]) > 0
 
 
 def test_bench_wmma_exact_on_fp16_inputs():

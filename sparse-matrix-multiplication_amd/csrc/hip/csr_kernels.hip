@@ -1119,10 +1119,12 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
     slice_cols = ceil_div(slice_cols, vec) * vec;
     const int groups = pick_groups(slice_cols, vec, want_groups);
     // Defaults measured on MI355X (c1 / c2 / c5 and uniform / power-law
-    // sweeps): 8 waves per workgroup without column slices, 4 with them (the
-    // sliced launch has twice the workgroups per row block), 4 entries per
-    // group in flight per step (two steps in flight), about 160 nonzeros per
-    // wave and at least 512 workgroups (two per CU) when the matrix allows it.
+    // sweeps): 8 waves per workgroup without column slices (a workgroup's
+    // nonzeros are split over its waves, so a long row is shared by eight),
+    // 4 with them (the sliced launch has twice the workgroups per row block),
+    // 4 entries per group in flight per step (two steps in flight), about 160
+    // nonzeros per wave and at least 512 workgroups (two per CU) when the
+    // matrix allows it: many small workgroups keep skewed rows balanced.
     // Rows known to be even (max_row_hint): the whole-round grid of 4-wave
     // workgroups.
     const bool even = split == nullptr && bounds == nullptr && o.rows_per_block <= 0 &&

@@ -215,6 +215,14 @@ int spmm_c_nnz_split_rows(const spmm_csr_t* h, int parts, int* h_rows_out);
 int spmm_c_split_partition_parts(int nnz);
 int spmm_c_tiled_v3_split(const spmm_csr_t* d_A, const int* d_split_rows, int parts,
                           const float* d_B, float* d_C, int N, float* d_carry, void* stream);
+/* The CSR form spmm_hybrid_run's CSR branch picks for host CSR h and a B of N
+ * columns (no counterpart in the reference): *form_out = 0 the row-block
+ * engine, 1 sub-wave row groups, 2 the merge-path partition; *opts_out the
+ * launch options for spmm_c_tiled_v3_opts (forms 0 and 1: the longest row as
+ * max_row_hint, row_groups = 1 for form 1); *parts_out the merge-path parts
+ * (form 2, else 0).  Host only. */
+int spmm_c_csr_auto_form(const spmm_csr_t* h, int N, int* form_out,
+                         spmm_engine_opts_t* opts_out, int* parts_out);
 /* spmm_tiled_v3 with explicit engine options (no reference counterpart). */
 int spmm_c_tiled_v3_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
                          const spmm_engine_opts_t* opts, void* stream);

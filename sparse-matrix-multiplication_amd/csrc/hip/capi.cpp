@@ -598,6 +598,25 @@ int spmm_c_tiled_v3_split(const spmm_csr_t* d_A, const int* d_split_rows, int pa
 
 int spmm_c_split_partition_parts(int nnz) { return spmm::engine::split_partition_parts(nnz); }
 
+int spmm_c_csr_auto_form(const spmm_csr_t* h, int N, int* form_out, spmm_engine_opts_t* opts_out,
+                         int* parts_out) {
+    if (h == nullptr || form_out == nullptr || opts_out == nullptr || parts_out == nullptr) {
+        return set_error(SPMM_INVALID, "null argument");
+    }
+    if (N < 0 || h->num_rows < 0 || h->nnz < 0 || (h->num_rows > 0 && h->row_ptr == nullptr)) {
+        return set_error(SPMM_INVALID, "bad CSR or N");
+    }
+    const spmm::engine::CsrChoice ch = spmm::engine::choose_csr_form(to_cpp(*h), N);
+    *form_out  = ch.form == spmm::engine::CsrForm::RowGroups ? 1
+                 : ch.form == spmm::engine::CsrForm::Split   ? 2
+                                                             : 0;
+    *opts_out  = spmm_engine_opts_t{};
+    opts_out->row_groups   = ch.opts.row_groups;
+    opts_out->max_row_hint = ch.opts.max_row_hint;
+    *parts_out = ch.parts;
+    return ok();
+}
+
 int spmm_c_tiled_v3_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
                          const spmm_engine_opts_t* opts, void* stream) {
     if (d_A == nullptr) return set_error(SPMM_INVALID, "null argument");

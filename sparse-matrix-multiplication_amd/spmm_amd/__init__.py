@@ -129,6 +129,8 @@ _SIGNATURES = {
     "spmm_c_tiled_v3_split": (_int, [_P(CsrT), _vp, _int, _vp, _vp, _int, _vp, _vp]),
     "spmm_c_launch_repeat_split": (_int, [_P(CsrT), _vp, _int, _vp, _vp, _int, _vp, _int, _vp]),
     "spmm_c_default_partition_parts": (_int, [_int, _int]),
+    "spmm_c_csr_auto_form": (_int, [_P(CsrT), _int, _P(ctypes.c_int),
+                                    _P(EngineOptsT), _P(ctypes.c_int)]),
     "spmm_c_tiled_v3_opts": (_int, [_P(CsrT), _vp, _vp, _int, _P(EngineOptsT), _vp]),
     "spmm_c_float_to_half": (_int, [_vp, _vp, _long, _vp]),
     "spmm_c_wmma": (_int, [_P(BsrT), _vp, _vp, _int, _vp]),
@@ -404,6 +406,19 @@ def nnz_split_rows(m: HostCSR, parts: int) -> np.ndarray:
 
 def split_partition_parts(nnz: int) -> int:
     return int(lib().spmm_c_split_partition_parts(nnz))
+
+
+_CSR_FORMS = {0: "engine", 1: "rowgroups", 2: "split"}
+
+
+def csr_auto_form(m: HostCSR, N: int):
+    """The CSR form spmm_hybrid_run picks: (name, EngineOptsT, merge-path parts)."""
+    src = m.struct()
+    form, parts = ctypes.c_int(), ctypes.c_int()
+    opts = EngineOptsT()
+    _check(lib().spmm_c_csr_auto_form(ctypes.byref(src), N, ctypes.byref(form), ctypes.byref(opts),
+                                      ctypes.byref(parts)))
+    return _CSR_FORMS[form.value], opts, parts.value
 
 
 def compare(ours: np.ndarray, ref: np.ndarray):

@@ -241,6 +241,39 @@ def test_bsr_stats_from_csr_host_equals_full_build(S):
             assert getattr(fast, f) == getattr(full, f), f
 
 
+def test_csr_auto_form(S):
+    # the CSR form spmm_hybrid_run picks from the row lengths (host only):
+    # row groups, the engine with the longest row as hint, or merge-path
+    c1 = S.generate_uniform_random_csr(4096, 4096, 0.01, 42)
+    c2 = S.generate_uniform_random_csr(8192, 8192, 0.01, 42)
+    c5 = S.generate_power_law_csr(16384, 16384, 164.0, 1.5, 4096, 3003)
+    longest = lambda m: int(np.diff(m.row_ptr).max())
+    form, opts, parts = S.csr_auto_form(c1, 128)  # >= 4096 even rows at N = 128
+    assert (form, opts.row_groups, opts.max_row_hint, parts) == ("rowgroups", 1, longest(c1), 0)
+    form, opts, parts = S.csr_auto_form(c2, 128)  # 8192 rows of 82: the engine's one round
+    assert (form, opts.row_groups, opts.max_row_hint, parts) == ("engine", 0, longest(c2), 0)
+    form, opts, parts = S.csr_auto_form(c5, 128)  # a 4096-entry row: merge-path
+    assert (form, parts) == ("split", S.split_partition_parts(c5.nnz))
+    assert longest(c5) == 4096
+    assert S.csr_auto_form(c2, 16)[0] == "rowgroups"
+    assert S.csr_auto_form(c2, 256)[0] == "engine"
+    # N = 16: four column lanes take rows up to 16384 / 4 = 4096 entries
+    assert S.csr_auto_form(c5, 16)[0] == "rowgroups"
+    # N = 64: 16 column lanes, rows up to 1024 (or 8x the average) -> merge-path
+    assert S.csr_auto_form(c5, 64)[0] == "split"
+    # power-law rows capped at 512 pass the skew test but are not even: the engine
+    pl = S.generate_power_law_csr(16384, 16384, 164.0, 1.5, 512, 5)
+    assert longest(pl) <= 512
+    assert S.csr_auto_form(pl, 128)[0] == "engine"
+    assert S.csr_auto_form(pl, 16)[0] == "rowgroups"
+    # no nonzeros: the engine, no hint
+    empty = S.csr_from_coo_host(8, 8, [], [], [])
+    assert S.csr_auto_form(empty, 32)[:2][0] == "engine"
+    with pytest.raises(S.SpmmError) as e:
+        S.csr_auto_form(c1, -1)
+    assert e.value.code == S.SPMM_INVALID
+
+
 def test_nnz_split_rows_definition(S):
     # rows[g] = last row r < M with row_ptr[r] <= nnz*g/parts; rows[0] = 0, rows[parts] = M
     rng = np.random.default_rng(12)

@@ -98,7 +98,7 @@ typedef struct spmm_engine_opts_t {
                            chosen from the shape, 2: per-lane index loads,
                            3: cooperative index loads.  0: the engine, except
                            that default launches of tiled_v3 / tiled_v4 with
-                           N <= 8 (at most two 16-byte column lanes) take the
+                           N <= 16 (at most four 16-byte column lanes) take the
                            row groups */
     int entry_lanes;    /* row groups: entry lanes per row, power of two <= 64 */
     int max_row_hint;   /* longest row's entries if known (0 = unknown).

@@ -1082,18 +1082,22 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
     }
     const int vec = pick_vec(N, B, C, want_vec);
     // Default launches of the production roles at N of a few columns (at most
-    // two column lanes of VEC floats, e.g. N <= 8 with 16-byte lanes) take the
-    // sub-wave row groups: the engine keeps 3/4 or more of its lanes idle
-    // there, and with 128 or 256 entry lanes the row groups' workgroup-wide
-    // pass shares a long row among many lanes (measured on MI355X: 1.6 - 3.4x
-    // faster on uniform rows, 2.5 - 3.6x on power-law rows of up to 4096
-    // entries).  Any explicit engine option keeps the engine.
+    // four column lanes of VEC floats, e.g. N <= 16 with 16-byte lanes) take
+    // the sub-wave row groups: the engine keeps half or more of its lanes idle
+    // there, and with 64 .. 256 entry lanes the row groups' workgroup-wide
+    // pass shares a long row among many lanes.  Measured on MI355X without
+    // row-length knowledge: 1.6 - 3.4x faster on uniform rows at N <= 8 and
+    // 2.5 - 3.6x on power-law rows of up to 4096 entries; at N = 12 - 16 over
+    // 32 uniform and power-law inputs (M 2048 .. 65536) 2.0x on average, never
+    // slower (1.18x at worst).  At N = 24 - 32 the largest power-law inputs
+    // lose (0.79x), so wider B keeps the engine.  Any explicit engine option
+    // keeps the engine.
     const bool engine_defaults = o.vec == 0 && o.waves == 0 && o.unroll == 0 &&
                                  o.rows_per_block == 0 && o.groups == 0 && o.slices == 0 &&
                                  o.global_loads == 0 && o.entry_lanes == 0;
     if (o.row_groups == 0 && engine_defaults && bounds == nullptr && split == nullptr &&
         (role == CsrRole::TiledV3 || role == CsrRole::TiledV4) &&
-        b_fits_buffer(A.num_cols, N) && pow2_log_at_least(ceil_div(N, vec)) <= 1) {
+        b_fits_buffer(A.num_cols, N) && pow2_log_at_least(ceil_div(N, vec)) <= 2) {
         EngineOpts rg = o;
         rg.row_groups   = 1;
         rg.max_row_hint = 0;  // with row_groups = 0 the hint only ever chooses a grid

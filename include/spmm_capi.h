@@ -98,16 +98,19 @@ typedef struct spmm_engine_opts_t {
                            chosen from the shape, 2: per-lane index loads,
                            3: cooperative index loads.  0: the engine, except
                            that default launches of tiled_v3 / tiled_v4 with
-                           N <= 16 (at most four 16-byte column lanes) take the
+                           N <= 16 (at most four 16-byte column lanes), or
+                           N <= 32 on up to 4 M nonzeros, take the
                            row groups */
     int entry_lanes;    /* row groups: entry lanes per row, power of two <= 64 */
     int max_row_hint;   /* longest row's entries if known (0 = unknown).
                            row_groups != 0: lets the kernel drop its long-row
                            pass when no row needs it (a hint below the true
                            longest row gives wrong results for the longer rows).
-                           row_groups == 0: rows within 2 x average + 32 entries
-                           give the row-block engine a grid of whole rounds of
-                           4-wave workgroups; a wrong hint only costs time */
+                           row_groups == 0: the row-block engine (also for the
+                           narrow B that takes row groups by default); rows
+                           within 2 x average + 32 entries give it a grid of
+                           whole rounds of 4-wave workgroups; a wrong hint only
+                           costs time */
 } spmm_engine_opts_t;
 
 /* BSR matrix-core kernel tuning (0 = automatic).  No counterpart in the

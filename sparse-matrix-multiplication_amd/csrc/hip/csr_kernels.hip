@@ -1089,18 +1089,23 @@ Error launch_csr_impl(CsrRole role, const CSR& A, const float* B, float* C, int 
     // row-length knowledge: 1.6 - 3.4x faster on uniform rows at N <= 8 and
     // 2.5 - 3.6x on power-law rows of up to 4096 entries; at N = 12 - 16 over
     // 32 uniform and power-law inputs (M 2048 .. 65536) 2.0x on average, never
-    // slower (1.18x at worst).  At N = 24 - 32 the largest power-law inputs
-    // lose (0.79x), so wider B keeps the engine.  Any explicit engine option
-    // keeps the engine.
+    // slower (1.18x at worst).  Up to eight lanes (N <= 32) they win 1.07 -
+    // 1.75x on the inputs of up to 2.5 M nonzeros but lose 0.79 - 0.97x on
+    // power-law inputs of 4.6 M nonzeros and more, so five to eight lanes take
+    // them only up to 4 M nonzeros.  Any explicit engine option keeps the
+    // engine, and so does a longest-row hint: a caller that knows its rows
+    // (spmm_hybrid_run) chooses the form itself.
     const bool engine_defaults = o.vec == 0 && o.waves == 0 && o.unroll == 0 &&
                                  o.rows_per_block == 0 && o.groups == 0 && o.slices == 0 &&
-                                 o.global_loads == 0 && o.entry_lanes == 0;
+                                 o.global_loads == 0 && o.entry_lanes == 0 &&
+                                 o.max_row_hint == 0;
     if (o.row_groups == 0 && engine_defaults && bounds == nullptr && split == nullptr &&
         (role == CsrRole::TiledV3 || role == CsrRole::TiledV4) &&
-        b_fits_buffer(A.num_cols, N) && pow2_log_at_least(ceil_div(N, vec)) <= 2) {
+        b_fits_buffer(A.num_cols, N) &&
+        (pow2_log_at_least(ceil_div(N, vec)) <= 2 ||
+         (pow2_log_at_least(ceil_div(N, vec)) <= 3 && A.nnz <= (1 << 22)))) {
         EngineOpts rg = o;
-        rg.row_groups   = 1;
-        rg.max_row_hint = 0;  // with row_groups = 0 the hint only ever chooses a grid
+        rg.row_groups = 1;
         return launch_row_groups(A, B, C, N, stream, vec, rg);
     }
     if (o.row_groups != 0) {

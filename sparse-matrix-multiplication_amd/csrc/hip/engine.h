@@ -49,17 +49,18 @@ struct EngineOpts {
     // index-load form chosen from the shape, 2 per-lane index loads, 3
     // cooperative index loads handed out by shuffles.  0: the engine, except
     // that default launches of spmm_tiled_v3 / _v4 with at most four column
-    // lanes (N <= 16 with 16-byte lanes) take the row groups.
+    // lanes (N <= 16 with 16-byte lanes), or eight (N <= 32) on up to 4 M
+    // nonzeros, take the row groups.
     int row_groups     = 0;
     int entry_lanes    = 0;  // row groups: entry lanes per row, a power of two up to 64
     // The longest row's entries when the caller knows it (0 = unknown).
     // row_groups != 0: with no row longer than the long-row cut, the kernel
     // is built without its workgroup-wide pass; a hint below the true longest
-    // row gives wrong results for the longer rows.  row_groups == 0 (also
-    // where N <= 16 takes the row groups by default, which then ignore it):
-    // rows within 2 x average + 32 entries give the row-block engine's
-    // implicit partition a grid of whole rounds of 4-wave workgroups instead
-    // of ~160 entries per wave; a wrong hint only costs time.
+    // row gives wrong results for the longer rows.  row_groups == 0: the
+    // row-block engine (a hint also keeps narrow B off the default row
+    // groups); rows within 2 x average + 32 entries give its implicit
+    // partition a grid of whole rounds of 4-wave workgroups instead of ~160
+    // entries per wave; a wrong hint only costs time.
     int max_row_hint   = 0;
 };
 

@@ -142,7 +142,7 @@ def _long_row_csr(S, rng, M, K):
 def test_row_groups_random(S, O, torch, chunk):
     # the sub-wave row groups under random shapes, skew, load forms, column
     # slices, entry lanes, unroll and longest-row hints (exact or above the
-    # true longest row), plus the default launch (row groups for N <= 16)
+    # true longest row), plus the default launch (row groups for N <= 32)
     rng = np.random.default_rng(3000 + chunk)
     for case in range(40):
         M = int(rng.integers(1, 1500))

@@ -67,6 +67,7 @@ def _shape(rng):
 @pytest.mark.parametrize("chunk", range(4))
 def test_csr_engine_random(S, O, torch, chunk):
     rng = np.random.default_rng(1000 + chunk)
+    hint_rng = np.random.default_rng(5000 + chunk)
     for case in range(30):
         M, K, N = _shape(rng)
         A = _random_csr(S, rng, M, K)
@@ -77,7 +78,16 @@ def test_csr_engine_random(S, O, torch, chunk):
                              int(rng.choice([0, 1, 2, 4, 8])), int(rng.choice([0, 1, 2, 4, 8])),
                              int(rng.choice([0, 0, 1])), int(rng.choice([0, 0, 1, 2, 3])),
                              int(rng.choice([0, 1, 2, 8, 64])))
+        # a longest-row hint from its own stream (the draws above stay as they
+        # were): true, above it, or -- for the engine only, where it just
+        # chooses the grid -- below it
+        longest = int(np.diff(A.row_ptr).max()) if M and A.nnz else 0
+        kinds = ["none", "true", "high"] + (["low"] if opts.row_groups == 0 else [])
+        kind = kinds[int(hint_rng.integers(0, len(kinds)))]
+        opts.max_row_hint = {"none": 0, "true": longest, "high": 2 * longest + 40,
+                             "low": 1}[kind]
         say(f"fuzz csr chunk={chunk} case={case} M={M} K={K} N={N} nnz={A.nnz} "
+            f"hint={kind}:{opts.max_row_hint} "
             f"opts=({opts.vec},{opts.waves},{opts.unroll},{opts.rows_per_block},{opts.groups},"
             f"{opts.slices},{opts.global_loads},{opts.row_groups},{opts.entry_lanes})")
         C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)

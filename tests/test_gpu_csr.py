@@ -347,6 +347,26 @@ def test_engine_whole_round_grid(S, O, torch, edge_cases, hint_kind):
     check_csr(_run_opts(S, torch, A, B, S.EngineOptsT(0, 0, 0, 0, 0, 0, 0, 0, 0, hint)), C64, absC)
 
 
+@pytest.mark.parametrize("N", [8, 12, 16, 24, 32, 40])
+def test_default_narrow_b(S, O, torch, N):
+    # plain spmm_tiled_v3 / _v4 at narrow B: row groups by default up to four
+    # 16-byte column lanes, and up to eight on up to 4 M nonzeros (the
+    # engine above that and for N = 40); tall uniform and power-law matrices
+    rng = np.random.default_rng(60 + N)
+    mats = [S.generate_uniform_random_csr(70000, 4096, 6.0 / 4096, 61),
+            S.generate_power_law_csr(20000, 20000, 30.0, 1.5, 4096, 62)]
+    for A in mats:
+        B = rng.uniform(-1, 1, (A.num_cols, N)).astype(np.float32)
+        C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)
+        for kernel in ("tiled_v3", "tiled_v4"):
+            say(f"csr default narrow {kernel} M={A.num_rows} K={A.num_cols} N={N} nnz={A.nnz}")
+            dA = S.DeviceCSR(A)
+            dC = torch.full((A.num_rows, N), float("nan"), device="cuda")
+            S.spmm_csr(kernel, dA, torch.from_numpy(B).cuda(), dC)
+            torch.cuda.synchronize()
+            check_csr(dC.cpu().numpy(), C64, absC)
+
+
 @pytest.mark.parametrize("slices", [2, 4, 8])
 def test_row_groups_column_slices(S, torch, edge_cases, slices):
     # XCD-tied column slices: each workgroup computes 1/slices of the columns

@@ -1,19 +1,31 @@
-"""Headline benchmark: CSR SpMM on BASELINE config c2 (uniform 8192 x 8192,
-density 0.01, N = 128, fp32), the configuration the metric is quoted on.
+"""Headline benchmark: SpMM per BASELINE pattern at m = 8192 (c2 is `value`).
 
-One step = one pass of the hot path (one spmm_tiled_v3 launch, the CSR engine
-the hybrid dispatcher picks for c2) over inputs already resident in HBM.
-W untimed steps, then K steps launched back to back on torch's current stream
-between two events on that stream (synchronised on both sides), through the
-engine's C ABI.  Prints one JSON line.
+The metric is "SpMM GFLOP/s (2*nnz*N/t) + % HBM/MFMA roofline, m=8192 per
+pattern".  `value` is c2 (uniform 8192 x 8192, density 0.01, N = 128, fp32),
+the configuration the metric is quoted on; `patterns` holds one block per
+BASELINE config (c1 .. c5), each timed the way spmm_hybrid_run runs it: the
+backend hybrid_choose picks (reference spmm_hybrid.cu:32-56), and for CSR the
+form the hybrid's CSR branch picks (row-block engine with the longest row as
+hint, sub-wave row groups, or the merge-path partition).
 
-roofline.achieved = compulsory bytes per launch (scripts/roofline.py:177-185:
-8*nnz + 4*(M+1) + 4*K*N + 4*M*N) / average launch time.  roofline.traffic is the
-HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
-scaled by the copy-kernel calibration), read from profiles/traffic_c2.json when
-present.  roofline.measured_copy is the rate a 256 MiB device-to-device copy
-reaches on the same GPU, with achieved / that rate.  cpu_baseline times the CPU
-oracle's fp64 loop (oracle/) on the same matrix on the host cores.
+One step = one pass of the hot path over inputs already resident in HBM
+(for the merge-path form: its engine launch plus its carry fix-up).  W untimed
+steps, then K steps back to back on torch's current stream between two events
+on that stream, synchronised on both sides.  `cold_ms_median` is the median of
+single launches each preceded by a 512 MiB write that evicts L2 (4 MiB per
+XCD) and the 256 MB MALL; warm is the contract figure.
+
+Roofline units (scripts/roofline.py:177-185, harness.cu:239,278-280):
+  CSR bytes = 8*nnz + 4*(M+1) + 4*K*N + 4*M*N, FLOPs = 2*nnz*N
+  BSR bytes = 516*blocks + 4*(M/16+1) + 2*K*N + 4*M*N, executed MFMA FLOPs =
+  2*256*blocks*N (GFLOP/s uses the original nnz, as the reference does).
+`traffic` = HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE
+(profiles/traffic_<cfg>.json, scaled by a plain-copy calibration), published
+only while the kernel sources hash to what they were at capture; otherwise
+null with the reason.  cpu_baseline times the CPU oracle (oracle/, test
+infrastructure used here only as the reported baseline) on the same inputs on
+all host threads this process may use (at most 16, the CPU share of one GPU on
+the MI355X boxes) and on one thread.
 """
 from __future__ import annotations
 
@@ -25,44 +37,188 @@ import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.join(ROOT, "sparse-matrix-multiplication_amd")
-HBM_PEAK_GBS = 8000.0
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E datasheet
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA datasheet
 COPY_BYTES = 256 * 1024 * 1024
+FLUSH_BYTES = 512 * 1024 * 1024
+METRIC = "SpMM GFLOP/s (2*nnz*N/t) + % HBM/MFMA roofline, m=8192 per pattern"
+HEADLINE = "c2"
+ORDER = ("c1", "c2", "c3", "c4", "c5")
 
-WORKLOAD = {"workload": "c2: uniform-random CSR 8192x8192 density 0.01, B 8192x128 fp32, "
-                        "C = A*B fp32, kernel spmm_tiled_v3 (CSR engine)",
-            "m": 8192, "k": 8192, "n": 128, "density": 0.01, "seed_a": 42, "seed_b": 43}
+
+def host_threads() -> int:
+    return max(1, min(16, len(os.sched_getaffinity(0))))
 
 
-def cpu_baseline(A, B, flops: float, budget_s: float = 12.0):
-    """Time the oracle's fp64 CSR loop (test infrastructure, used here only as
-    the reported CPU baseline) on the same matrix, all host threads up to 16."""
+def _median(v):
+    v = sorted(v)
+    return v[len(v) // 2]
+
+
+def _time_cpu(fn, budget_s: float, min_runs: int):
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return _median(times), len(times)
+
+
+def cpu_baseline(P, flops: float, budget_s: float = 2.5):
+    """The oracle's loop on the same inputs: fp64-accumulated CSR x dense for
+    CSR patterns, fp32 accumulation of the fp16 operands for BSR patterns."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import numpy as np
     import oracle_lib as O
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    rp = np.ascontiguousarray(A.row_ptr, np.int32)
-    ci = np.ascontiguousarray(A.col_idx, np.int32)
-    va = np.ascontiguousarray(A.values, np.float32)
-    Bc = np.ascontiguousarray(B, np.float32)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        O.csr_spmm_f64(rp, ci, va, Bc, threads=threads, with_abs=False)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 200:
-            break
-    times.sort()
-    med = times[len(times) // 2]
-    return {"value": flops / med / 1e9, "unit": "GFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"full c2 workload (oracle fp64 CSR x dense, {threads} threads), "
-                      f"median of {len(times)} runs, {med * 1e3:.2f} ms each"}
+    if P["backend"] == "wmma":
+        hb, B16 = P["host_bsr"], O.f32_to_f16(P["B"])
+        kind = "oracle fp32-accumulate BSR x fp16 dense"
+
+        def run(threads):
+            return lambda: O.bsr_spmm_f32(P["M"], P["K"], hb.row_ptr, hb.col_idx, hb.values,
+                                          B16, threads=threads)
+    else:
+        A = P["host"]
+        rp = np.ascontiguousarray(A.row_ptr, np.int32)
+        ci = np.ascontiguousarray(A.col_idx, np.int32)
+        va = np.ascontiguousarray(A.values, np.float32)
+        Bc = np.ascontiguousarray(P["B"], np.float32)
+        kind = "oracle fp64-accumulate CSR x dense"
+
+        def run(threads):
+            return lambda: O.csr_spmm_f64(rp, ci, va, Bc, threads=threads, with_abs=False)
+    T = host_threads()
+    med_t, n_t = _time_cpu(run(T), budget_s, 3)
+    med_1, n_1 = _time_cpu(run(1), budget_s, 1)
+    return {"value": round(flops / med_t / 1e9, 2), "unit": "GFLOP/s", "cores": T,
+            "kind": "port", "ms": round(med_t * 1e3, 3),
+            "one_thread": {"value": round(flops / med_1 / 1e9, 2), "unit": "GFLOP/s",
+                           "cores": 1, "ms": round(med_1 * 1e3, 3)},
+            "sample": f"full {P['name']} workload ({kind}); median of {n_t} runs on {T} threads "
+                      f"and of {n_1} on 1 thread; host reports {os.cpu_count()} CPUs, "
+                      f"{len(os.sched_getaffinity(0))} in this process's affinity"}
 
 
-def measured_copy_gbs(torch, stream, reps: int = 20) -> float:
+def load_traffic(name: str, backend: str, kernel: str):
+    """HBM bytes per launch for `name` if profiles/traffic_<name>.json was
+    captured on the current kernel sources; else (None, reason)."""
+    from spmm_amd.traffic import sources_sha256
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(path):
+        return None, "no capture"
+    with open(path) as f:
+        t = json.load(f)
+    if t.get("sources_sha256") != sources_sha256(backend):
+        return None, f"stale: captured at {t.get('commit', '?')} on other kernel sources"
+    if t.get("form") != kernel:
+        return None, f"stale: captured on form {t.get('form')!r}, now {kernel!r}"
+    return t.get("hbm_bytes_per_launch"), f"rocprofv3 FETCH_SIZE + WRITE_SIZE at {t.get('commit')}"
+
+
+def build_pattern(S, torch, name: str):
+    """Inputs in HBM and a launch(reps) closure for the form the hybrid picks."""
+    from spmm_amd.configs import CONFIGS, make_config
+    pattern, M, N, fp16, desc = CONFIGS[name]
+    A, B = make_config(S, name)
+    plan = S.hybrid_choose(A, N)
+    stream = torch.cuda.current_stream()
+    C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    P = {"name": name, "M": M, "K": A.num_cols, "N": N, "nnz": A.nnz, "host": A, "B": B,
+         "desc": desc, "backend": plan.backend_name, "C": C,
+         "fill_in": round(plan.fill_in_ratio, 4)}
+    if plan.backend == S.BACKEND_WMMA:
+        hb = S.bsr_from_csr_host(A)
+        dA = S.DeviceBSR(hb)
+        B16 = S.float_to_half(torch.from_numpy(B).cuda())
+        P.update(host_bsr=hb, blocks=hb.num_blocks, form="wmma", dtype="f16 in, f32 accumulate")
+        P["launch"] = lambda reps: S.launch_repeat("wmma", dA, B16, C, reps, stream)
+        P["keep"] = (dA, B16)
+        return P
+    form, opts, parts = S.csr_auto_form(A, N)
+    dA = S.DeviceCSR(A)
+    dB = torch.from_numpy(B).cuda()
+    P.update(form=form, dtype="f32")
+    if form == "split":
+        rows = torch.from_numpy(S.nnz_split_rows(A, parts)).cuda()
+        carry = torch.empty((parts, N), dtype=torch.float32, device="cuda")
+        P["parts"] = parts
+        P["launch"] = lambda reps: S.launch_repeat_split(dA, rows, dB, C, carry, reps, stream)
+        P["keep"] = (dA, dB, rows, carry)
+    else:
+        P["launch"] = lambda reps: S.launch_repeat_opts(dA, dB, C, opts, reps, stream)
+        P["keep"] = (dA, dB)
+    return P
+
+
+def time_warm(torch, P, steps: int, warmup: int) -> float:
+    stream = torch.cuda.current_stream()
+    P["launch"](max(warmup, 1))
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    P["launch"](steps)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps
+
+
+def time_cold(torch, P, flush, reps: int = 15) -> float:
+    """Median of single launches, each after a 512 MiB write (L2 and MALL evicted)."""
+    stream = torch.cuda.current_stream()
+    evs = []
+    for i in range(reps):
+        flush.fill_(float(i))
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        P["launch"](1)
+        e1.record(stream)
+        evs.append((e0, e1))
+    torch.cuda.synchronize()
+    return _median([a.elapsed_time(b) for a, b in evs])
+
+
+def pattern_block(P, ms: float, cold_ms: float):
+    M, K, N, nnz = P["M"], P["K"], P["N"], P["nnz"]
+    sec = ms * 1e-3
+    flops = 2.0 * nnz * N
+    blk = {"workload": P["desc"], "backend": P["backend"], "form": P["form"], "nnz": nnz,
+           "N": N, "fill_in": P["fill_in"], "dtype": P["dtype"], "ms_per_step": round(ms, 6),
+           "cold_ms_median": None if cold_ms is None else round(cold_ms, 6),
+           "gflops": round(flops / sec / 1e9, 2)}
+    if P["backend"] == "wmma":
+        nb = P["blocks"]
+        alg = 516.0 * nb + 4.0 * ((M + 15) // 16 + 1) + 2.0 * K * N + 4.0 * M * N
+        exec_flops = 2.0 * 256 * nb * N
+        tf = exec_flops / sec / 1e12
+        hbm = alg / sec / 1e9
+        traffic, note = load_traffic(P["name"], "wmma", P["form"])
+        blk["blocks"] = nb
+        blk["roofline"] = {"bound": "mfma", "achieved": round(tf, 2),
+                           "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                           "frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                           "exec_flops": exec_flops, "traffic": traffic, "traffic_source": note,
+                           "hbm": {"achieved": round(hbm, 1), "peak": HBM_PEAK_GBS,
+                                   "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4),
+                                   "alg_bytes": alg}}
+    else:
+        alg = 8.0 * nnz + 4.0 * (M + 1) + 4.0 * K * N + 4.0 * M * N
+        hbm = alg / sec / 1e9
+        traffic, note = load_traffic(P["name"], "csr", P["form"])
+        if "parts" in P:
+            blk["parts"] = P["parts"]
+        blk["roofline"] = {"bound": "hbm", "achieved": round(hbm, 1), "peak": HBM_PEAK_GBS,
+                           "unit": "GB/s", "frac": round(hbm / HBM_PEAK_GBS, 4),
+                           "alg_bytes": alg, "traffic": traffic, "traffic_source": note}
+    return blk, flops
+
+
+def measured_copy_gbs(torch, reps: int = 20) -> float:
     """HBM rate a plain 256 MiB device-to-device copy reaches on this GPU
-    (read + write bytes per second): the measured counterpart of the 8 TB/s
-    datasheet peak, reported beside it."""
+    (read + write bytes per second), reported beside the datasheet peak."""
+    stream = torch.cuda.current_stream()
     src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -76,7 +232,6 @@ def measured_copy_gbs(torch, stream, reps: int = 20) -> float:
     e1.record(stream)
     torch.cuda.synchronize()
     sec = e0.elapsed_time(e1) * 1e-3 / reps
-    del src, dst
     return 2.0 * COPY_BYTES / sec / 1e9
 
 
@@ -84,8 +239,7 @@ def copy_calibration(steps: int) -> int:
     """A plain copy of known size: reads and writes exactly COPY_BYTES per launch."""
     import torch
     torch.cuda.set_device(0)
-    n = COPY_BYTES // 4
-    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(steps):
         dst.copy_(src)
@@ -99,7 +253,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache timings")
+    ap.add_argument("--only", default="",
+                    help="comma-separated subset of c1..c5 (profiling runs); the headline "
+                         "line needs c2")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 256 MiB device-to-device copy, --steps times (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -111,6 +269,7 @@ def main() -> int:
               "supported (the row-sharded multi-GPU split is a design note only)",
               file=sys.stderr)
         return 2
+    names = [n for n in ORDER if not args.only or n in args.only.split(",")]
 
     sys.path.insert(0, PKG_DIR)
     import torch
@@ -120,64 +279,59 @@ def main() -> int:
     torch.cuda.set_device(0)
     S.lib()
 
-    m, k, n = WORKLOAD["m"], WORKLOAD["k"], WORKLOAD["n"]
-    A = S.generate_uniform_random_csr(m, k, WORKLOAD["density"], WORKLOAD["seed_a"])
-    B = S.generate_dense_row_major(k, n, WORKLOAD["seed_b"])
-    dA = S.DeviceCSR(A)
-    dB = torch.from_numpy(B).cuda()
-    dC = torch.empty((m, n), dtype=torch.float32, device="cuda")
-    stream = torch.cuda.current_stream()
+    flush = None if args.no_cold else torch.empty(FLUSH_BYTES // 4, dtype=torch.float32,
+                                                  device="cuda")
+    blocks = {}
+    for name in names:
+        P = build_pattern(S, torch, name)
+        ms = time_warm(torch, P, args.steps, args.warmup)
+        cold = time_cold(torch, P, flush) if flush is not None else None
+        blk, flops = pattern_block(P, ms, cold)
+        if not args.no_cpu:
+            blk["cpu_baseline"] = cpu_baseline(P, flops)
+        blocks[name] = blk
+        print(f"bench: {name} {P['backend']}/{P['form']} {ms * 1e3:.2f} us warm "
+              f"{(cold or 0) * 1e3:.2f} us cold {blk['gflops']:.0f} GFLOP/s", file=sys.stderr,
+              flush=True)
+        del P
+    del flush
+    if HEADLINE not in blocks:
+        print(json.dumps({"patterns": blocks}), flush=True)
+        return 0
 
-    S.launch_repeat("tiled_v3", dA, dB, dC, max(args.warmup, 1), stream)
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ev0.record(stream)
-    S.launch_repeat("tiled_v3", dA, dB, dC, args.steps, stream)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    total_ms = ev0.elapsed_time(ev1)
-    ms = total_ms / args.steps
-
-    nnz = A.nnz
-    flops = 2.0 * nnz * n
-    gflops = flops / (ms * 1e-3) / 1e9
-    alg_bytes = 8.0 * nnz + 4.0 * (m + 1) + 4.0 * k * n + 4.0 * m * n
-    achieved = alg_bytes / (ms * 1e-3) / 1e9
-
-    copy_gbs = measured_copy_gbs(torch, stream)
-
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic_c2.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
-
+    h = blocks[HEADLINE]
+    copy_gbs = measured_copy_gbs(torch)
+    roof = dict(h["roofline"])
+    roof["measured_copy"] = {"value": round(copy_gbs, 1), "unit": "GB/s",
+                             "frac": round(roof["achieved"] / copy_gbs, 4),
+                             "what": "256 MiB device-to-device copy on this GPU, "
+                                     "read + write bytes / time"}
+    from spmm_amd.configs import CONFIGS
+    _, M, N, _, desc = CONFIGS[HEADLINE]
     line = {
-        "metric": "SpMM GFLOP/s (2*nnz*N/t) + % HBM/MFMA roofline, m=8192 per pattern",
-        "value": round(gflops, 2),
+        "metric": METRIC,
+        "value": h["gflops"],
         "unit": "GFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 6),
+        "ms_per_step": h["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (reference generator: mt19937 seed 42 Bernoulli CSR, seed 43 dense B)",
-        "config": dict(WORKLOAD, nnz=nnz),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": traffic,
-                     "measured_copy": {"value": round(copy_gbs, 1), "unit": "GB/s",
-                                       "frac": round(achieved / copy_gbs, 4),
-                                       "what": "256 MiB device-to-device copy on this GPU, "
-                                               "read + write bytes / time"}},
+        "data": "synthetic (reference generator: mt19937 seed 42 Bernoulli CSR, seed 43 dense "
+                "B; structured patterns from fixed seeds)",
+        "config": {"workload": f"{HEADLINE}: {desc}, C = A*B fp32, the CSR form "
+                               f"spmm_hybrid_run picks ({h['form']})",
+                   "m": M, "k": M, "n": N, "density": 0.01, "seed_a": 42, "seed_b": 43,
+                   "nnz": h["nnz"]},
+        "roofline": roof,
+        "cold_ms_median": h["cold_ms_median"],
     }
-    if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(A, B, flops)
+    if "cpu_baseline" in h:
+        line["cpu_baseline"] = h["cpu_baseline"]
+    line["patterns"] = blocks
     print(json.dumps(line), flush=True)
     return 0
 

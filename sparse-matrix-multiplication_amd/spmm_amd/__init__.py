@@ -482,10 +482,19 @@ def gpu_count() -> int:
     return int(lib().spmm_c_gpu_count())
 
 
+def _host_b(m: HostCSR, B) -> np.ndarray:
+    """Host B as a contiguous float32 K x N array with K = A's columns (the C++
+    side copies K * N floats from it)."""
+    B = np.ascontiguousarray(B, dtype=np.float32)
+    if B.ndim != 2 or B.shape[0] != m.num_cols:
+        raise SpmmError(SPMM_INVALID, f"B: shape {B.shape}, expected ({m.num_cols}, N)")
+    return B
+
+
 def unified_run(m: HostCSR, B: np.ndarray, warmup: int = 3, iters: int = 10):
     """Reference spmm_unified (spmm_multigpu.cu:122-182): host in, host out ->
     (C, median ms, prefetched)."""
-    B = np.ascontiguousarray(B, dtype=np.float32)
+    B = _host_b(m, B)
     N = B.shape[1]
     C = np.empty((m.num_rows, N), dtype=np.float32)
     ms = ctypes.c_float()
@@ -498,7 +507,7 @@ def unified_run(m: HostCSR, B: np.ndarray, warmup: int = 3, iters: int = 10):
 
 def hybrid_run(plan: Plan, m: HostCSR, B: np.ndarray, warmup: int = 3, iters: int = 10):
     """Reference spmm_hybrid.cu:58-125: host in, host out -> (C, median ms)."""
-    B = np.ascontiguousarray(B, dtype=np.float32)
+    B = _host_b(m, B)
     N = B.shape[1]
     C = np.empty((m.num_rows, N), dtype=np.float32)
     p = HybridPlanT(plan.backend, plan.fill_in_ratio, plan.block_density, plan.threshold,
@@ -522,6 +531,54 @@ def _stream_handle(stream=None) -> int:
     torch = _torch()
     s = stream if stream is not None else torch.cuda.current_stream()
     return int(s.cuda_stream)
+
+
+
+def _device_of(A):
+    """The device holding a DeviceCSR / DeviceBSR's arrays (None for a library-built BSR)."""
+    rp = getattr(A, "row_ptr", None)
+    return rp.device if rp is not None and hasattr(rp, "device") else None
+
+
+def _check_dense(t, name: str, dtypes, rows: Optional[int] = None, cols: Optional[int] = None,
+                 device=None, ndim: int = 2):
+    """Validate a device operand before any launch: a contiguous cuda tensor of
+    one of `dtypes` with the expected shape.  The C ABI takes bare pointers and
+    sizes, so a wrong tensor here would otherwise read or write out of bounds
+    on the device; raises SpmmError(SPMM_INVALID) instead."""
+    torch = _torch()
+    if not isinstance(t, torch.Tensor):
+        raise SpmmError(SPMM_INVALID, f"{name}: expected a torch tensor, got {type(t).__name__}")
+    if not t.is_cuda:
+        raise SpmmError(SPMM_INVALID, f"{name}: must be a cuda tensor (got {t.device})")
+    if device is not None and t.device != device:
+        raise SpmmError(SPMM_INVALID, f"{name}: on {t.device}, the matrix is on {device}")
+    if t.dtype not in dtypes:
+        want = " or ".join(str(d) for d in dtypes)
+        raise SpmmError(SPMM_INVALID, f"{name}: dtype {t.dtype}, expected {want}")
+    if not t.is_contiguous():
+        raise SpmmError(SPMM_INVALID, f"{name}: must be contiguous (row-major)")
+    if t.dim() != ndim:
+        raise SpmmError(SPMM_INVALID, f"{name}: expected {ndim}-D, got shape {tuple(t.shape)}")
+    if rows is not None and int(t.shape[0]) != rows:
+        raise SpmmError(SPMM_INVALID, f"{name}: {int(t.shape[0])} rows, expected {rows}")
+    if cols is not None and ndim == 2 and int(t.shape[1]) != cols:
+        raise SpmmError(SPMM_INVALID, f"{name}: {int(t.shape[1])} columns, expected {cols}")
+
+
+def _csr_operands(A, B, C, fp16: bool = False):
+    """Check B (K x N) and C (M x N, float32; allocated when None) against A;
+    returns (N, C).  fp16: B holds fp16 values (float16, or int16 bit patterns)."""
+    torch = _torch()
+    dev = _device_of(A)
+    bt = (torch.float16, torch.int16) if fp16 else (torch.float32,)
+    _check_dense(B, "B", bt, rows=A.num_cols, device=dev)
+    N = int(B.shape[1])
+    if C is None:
+        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B.device)
+    else:
+        _check_dense(C, "C", (torch.float32,), rows=A.num_rows, cols=N, device=B.device)
+    return N, C
 
 
 class DeviceCSR:
@@ -614,9 +671,7 @@ def spmm_csr(kernel: str, A: DeviceCSR, B, C=None, stream=None):
     torch = _torch()
     if kernel not in CSR_KERNELS:
         raise SpmmError(SPMM_INVALID, f"unknown CSR kernel {kernel!r}")
-    N = int(B.shape[1]) if B.dim() == 2 else 0
-    if C is None:
-        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B.device)
+    N, C = _csr_operands(A, B, C)
     s = A.struct()
     fn = getattr(lib(), f"spmm_c_{kernel}")
     _check(fn(ctypes.byref(s), B.data_ptr(), C.data_ptr(), N, _stream_handle(stream)))
@@ -625,9 +680,10 @@ def spmm_csr(kernel: str, A: DeviceCSR, B, C=None, stream=None):
 
 def spmm_tiled_v3_partitioned(A: DeviceCSR, bounds, B, C=None, stream=None):
     torch = _torch()
-    N = int(B.shape[1])
-    if C is None:
-        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B.device)
+    N, C = _csr_operands(A, B, C)
+    _check_dense(bounds, "bounds", (torch.int32,), device=B.device, ndim=1)
+    if bounds.numel() < 2:
+        raise SpmmError(SPMM_INVALID, "bounds: needs parts + 1 >= 2 entries")
     s = A.struct()
     _check(lib().spmm_c_tiled_v3_partitioned(ctypes.byref(s), bounds.data_ptr(),
                                              int(bounds.numel()) - 1, B.data_ptr(),
@@ -638,10 +694,8 @@ def spmm_tiled_v3_partitioned(A: DeviceCSR, bounds, B, C=None, stream=None):
 def spmm_tiled_v3_split(A: DeviceCSR, split_rows, B, C=None, carry=None, stream=None):
     """Merge-path partition: split_rows = cuda int32 tensor of parts+1 rows."""
     torch = _torch()
-    N = int(B.shape[1])
-    parts = int(split_rows.numel()) - 1
-    if C is None:
-        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B.device)
+    N, C = _csr_operands(A, B, C)
+    parts = _check_split(split_rows, B, N, carry)
     if carry is None:
         carry = torch.empty((max(parts, 1), max(N, 1)), dtype=torch.float32, device=B.device)
     s = A.struct()
@@ -651,8 +705,27 @@ def spmm_tiled_v3_split(A: DeviceCSR, split_rows, B, C=None, carry=None, stream=
     return C
 
 
+def _check_split(split_rows, B, N: int, carry) -> int:
+    """Check the merge-path row table and carry workspace; returns parts."""
+    torch = _torch()
+    _check_dense(split_rows, "split_rows", (torch.int32,), device=B.device, ndim=1)
+    parts = int(split_rows.numel()) - 1
+    if parts < 1:
+        raise SpmmError(SPMM_INVALID, "split_rows: needs parts + 1 >= 2 entries")
+    if carry is not None:
+        _check_dense(carry, "carry", (torch.float32,), device=B.device, ndim=carry.dim())
+        if carry.numel() < parts * N:
+            raise SpmmError(SPMM_INVALID, f"carry: {carry.numel()} floats, needs parts * N = "
+                                          f"{parts * N}")
+    return parts
+
+
 def launch_repeat_split(A: DeviceCSR, split_rows, B, C, carry, reps: int, stream=None) -> None:
     """reps back-to-back merge-path launches (measurement helper)."""
+    N, C = _csr_operands(A, B, C)
+    _check_split(split_rows, B, N, carry)
+    if carry is None:
+        raise SpmmError(SPMM_INVALID, "carry: a workspace of parts * N floats is required")
     s = A.struct()
     _check(lib().spmm_c_launch_repeat_split(ctypes.byref(s), split_rows.data_ptr(),
                                             int(split_rows.numel()) - 1, B.data_ptr(),
@@ -661,10 +734,7 @@ def launch_repeat_split(A: DeviceCSR, split_rows, B, C, carry, reps: int, stream
 
 
 def spmm_tiled_v3_opts(A: DeviceCSR, B, opts: EngineOptsT, C=None, stream=None):
-    torch = _torch()
-    N = int(B.shape[1])
-    if C is None:
-        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B.device)
+    N, C = _csr_operands(A, B, C)
     s = A.struct()
     _check(lib().spmm_c_tiled_v3_opts(ctypes.byref(s), B.data_ptr(), C.data_ptr(), N,
                                       ctypes.byref(opts), _stream_handle(stream)))
@@ -674,8 +744,13 @@ def spmm_tiled_v3_opts(A: DeviceCSR, B, opts: EngineOptsT, C=None, stream=None):
 def float_to_half(src, dst=None, stream=None):
     """Reference spmm_wmma.cu:125-130: fp32 -> fp16 (RNE) on the device."""
     torch = _torch()
+    _check_dense(src, "src", (torch.float32,), ndim=src.dim() if hasattr(src, "dim") else 1)
     if dst is None:
         dst = torch.empty(src.shape, dtype=torch.float16, device=src.device)
+    else:
+        _check_dense(dst, "dst", (torch.float16, torch.int16), device=src.device, ndim=dst.dim())
+        if dst.numel() != src.numel():
+            raise SpmmError(SPMM_INVALID, f"dst: {dst.numel()} elements, src has {src.numel()}")
     _check(lib().spmm_c_float_to_half(src.data_ptr(), dst.data_ptr(), src.numel(),
                                       _stream_handle(stream)))
     return dst
@@ -683,10 +758,7 @@ def float_to_half(src, dst=None, stream=None):
 
 def spmm_wmma(A: DeviceBSR, B16, C=None, stream=None):
     """Reference spmm_wmma.cu:132-142: BSR x fp16 B -> fp32 C on matrix cores."""
-    torch = _torch()
-    N = int(B16.shape[1])
-    if C is None:
-        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B16.device)
+    N, C = _csr_operands(A, B16, C, fp16=True)
     s = A.struct()
     _check(lib().spmm_c_wmma(ctypes.byref(s), B16.data_ptr(), C.data_ptr(), N,
                              _stream_handle(stream)))
@@ -695,10 +767,7 @@ def spmm_wmma(A: DeviceBSR, B16, C=None, stream=None):
 
 def spmm_wmma_opts(A: DeviceBSR, B16, opts: BsrOptsT, C=None, stream=None):
     """spmm_wmma with explicit kernel options (row group, column tiles, per-wave)."""
-    torch = _torch()
-    N = int(B16.shape[1])
-    if C is None:
-        C = torch.empty((A.num_rows, N), dtype=torch.float32, device=B16.device)
+    N, C = _csr_operands(A, B16, C, fp16=True)
     s = A.struct()
     _check(lib().spmm_c_wmma_opts(ctypes.byref(s), B16.data_ptr(), C.data_ptr(), N,
                                   ctypes.byref(opts), _stream_handle(stream)))
@@ -706,6 +775,7 @@ def spmm_wmma_opts(A: DeviceBSR, B16, opts: BsrOptsT, C=None, stream=None):
 
 
 def launch_repeat_wmma_opts(A: DeviceBSR, B16, C, opts: BsrOptsT, reps: int, stream=None) -> None:
+    N, C = _csr_operands(A, B16, C, fp16=True)
     s = A.struct()
     _check(lib().spmm_c_launch_repeat_wmma_opts(ctypes.byref(s), B16.data_ptr(), C.data_ptr(),
                                                 int(B16.shape[1]), ctypes.byref(opts), reps,
@@ -713,12 +783,16 @@ def launch_repeat_wmma_opts(A: DeviceBSR, B16, C, opts: BsrOptsT, reps: int, str
 
 
 def launch_repeat(kernel: str, A, B, C, reps: int, stream=None) -> None:
+    if kernel not in KERNEL_IDS:
+        raise SpmmError(SPMM_INVALID, f"unknown kernel {kernel!r}")
+    N, C = _csr_operands(A, B, C, fp16=(kernel == "wmma"))
     s = A.struct()
     _check(lib().spmm_c_launch_repeat(KERNEL_IDS[kernel], ctypes.byref(s), B.data_ptr(),
                                       C.data_ptr(), int(B.shape[1]), reps, _stream_handle(stream)))
 
 
 def launch_repeat_opts(A: DeviceCSR, B, C, opts: EngineOptsT, reps: int, stream=None) -> None:
+    N, C = _csr_operands(A, B, C)
     s = A.struct()
     _check(lib().spmm_c_launch_repeat_opts(ctypes.byref(s), B.data_ptr(), C.data_ptr(),
                                            int(B.shape[1]), ctypes.byref(opts), reps,
@@ -727,6 +801,9 @@ def launch_repeat_opts(A: DeviceCSR, B, C, opts: EngineOptsT, reps: int, stream=
 
 def time_repeat(kernel: str, A, B, C, reps: int, stream=None) -> float:
     """Milliseconds for `reps` back-to-back launches between two hipEvents on `stream`."""
+    if kernel not in KERNEL_IDS:
+        raise SpmmError(SPMM_INVALID, f"unknown kernel {kernel!r}")
+    N, C = _csr_operands(A, B, C, fp16=(kernel == "wmma"))
     s = A.struct()
     ms = ctypes.c_float()
     _check(lib().spmm_c_time_repeat(KERNEL_IDS[kernel], ctypes.byref(s), B.data_ptr(),

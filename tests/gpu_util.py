@@ -4,37 +4,7 @@ from __future__ import annotations
 
 import numpy as np
 
-# Seeds: A uses 42 and B uses 43 (seed + 1), as harness.cu:304 does for the
-# uniform configs; the structured configs use their own fixed seeds.
-CONFIGS = {
-    # name: (pattern, M, N, fp16 operands)
-    "c1": ("uniform", 4096, 128, False),
-    "c2": ("uniform", 8192, 128, False),
-    "c3": ("banded", 8192, 128, True),
-    "c4": ("block_diagonal", 8192, 256, True),
-    "c5": ("power_law", 16384, 128, False),
-}
-
-
-def make_config(S, name: str):
-    """(HostCSR, B float32) of one BASELINE config, generated by the engine."""
-    pattern, M, N, fp16 = CONFIGS[name]
-    if pattern == "uniform":
-        A = S.generate_uniform_random_csr(M, M, 0.01, 42)
-        B = S.generate_dense_row_major(M, N, 43)
-    elif pattern == "banded":
-        A = S.generate_banded_csr(M, M, 64, 1003)
-        B = S.generate_dense_row_major(M, N, 1004)
-    elif pattern == "block_diagonal":
-        A = S.generate_block_diagonal_csr(M, M, 256, 2003, 0.1)
-        B = S.generate_dense_row_major(M, N, 2004)
-    else:
-        A = S.generate_power_law_csr(M, M, 164.0, 1.5, 4096, 3003)
-        B = S.generate_dense_row_major(M, N, 3004)
-    if fp16:
-        A.values = S.round_to_fp16(A.values)
-        B = S.round_to_fp16(B)
-    return A, B
+from spmm_amd.configs import CONFIGS, make_config  # noqa: F401  (the five BASELINE configs)
 
 
 def check_csr(C_gpu: np.ndarray, C64: np.ndarray, absC: np.ndarray, tol: float = 1e-5) -> float:

@@ -114,18 +114,22 @@ typedef struct spmm_engine_opts_t {
 } spmm_engine_opts_t;
 
 /* BSR matrix-core kernel tuning (0 = automatic).  No counterpart in the
- * reference: exposes the kernel's variants for measurement sweeps. */
+ * reference: exposes the kernels' variants for measurement sweeps.  Default:
+ * the shared-panel kernel on wide B with long structured block-rows (N >= 256,
+ * 24 - 64 blocks per block-row on average, K <= 131072), else the wave kernel. */
 typedef struct spmm_bsr_opts_t {
-    int row_group; /* 0: wave kernel (default); 1, 2, 4, 8: block-rows per
-                      workgroup sharing staged B tiles */
-    int tiles;     /* 16-column MFMA tiles per wave: 1, 2, 4 (8 with row groups) */
-    int per_wave;  /* 1: wave kernel whatever row_group says */
-    int depth;     /* wave kernel: block pairs in flight per wave: 1, 2, 4 */
-    int xcd_order; /* wave kernel: 0, 1 XCD-grouped workgroup order; 2 dispatch order */
-    int rows;      /* wave kernel: block-rows per wave sharing staged B tiles: 1, 2, 4 */
-    int split;     /* wave kernel: 4 = the four waves of a workgroup split one block-row */
-    int addressing; /* wave kernel: 0 B rows / A blocks as buffer records where they fit
-                       (tiles >= 2, N % 8 == 0), 1 pointer arithmetic */
+    int row_group;  /* 0: automatic; 1: wave kernel (one wave per block-row);
+                       4, 8: shared-panel kernel with that many block-rows per
+                       workgroup sharing staged B tiles */
+    int tiles;      /* wave kernel: 16-column MFMA tiles per wave, 1, 2, 4;
+                       panel kernel: 16-column tiles per workgroup, 4 or 8 */
+    int per_wave;   /* 1: wave kernel whatever row_group says */
+    int depth;      /* wave kernel: block pairs in flight per wave, 1, 2, 4;
+                       panel kernel: LDS stages in flight, 2 or 4 */
+    int xcd_order;  /* 0, 1 XCD-grouped workgroup order; 2 dispatch order */
+    int addressing; /* 0: B rows / A blocks as buffer records where they fit
+                       (N % 8 == 0, 16-byte aligned B); 1: pointer-arithmetic
+                       wave kernel */
 } spmm_bsr_opts_t;
 
 const char* spmm_c_last_error(void);

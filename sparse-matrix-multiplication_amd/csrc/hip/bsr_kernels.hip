@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "engine.h"
 #include "spmm/utils.h"
@@ -313,6 +314,13 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// Workgroup barrier without a memory fence: the caller has already waited
+// for the LDS writes (and buffer-to-LDS loads) its partners must see.  The
+// memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int J, int D>
 __device__ __forceinline__ void bsr_record_body(const BsrArgs& a, _Float16* __restrict__ s0,
                                                 _Float16* __restrict__ s1,
@@ -342,19 +350,30 @@ __device__ __forceinline__ void bsr_record_body(const BsrArgs& a, _Float16* __re
     const __amdgpu_buffer_rsrc_t rec_a = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<_Float16*>(a.vals), static_cast<short>(512), a.num_blocks, kBufWord3);
 
-    // Lane constants: load instruction c moves 16-byte chunk idx = lane + 64c,
-    // staged row srow (block srow >= 16 of the pair), columns n .. n+7 at byte
-    // offset nbyte of its B row, to slot offset 8 * idx fp16 (row-major).
-    // Columns past N read a valid chunk of the row instead; their products
-    // land in output columns >= N, which are never stored.
+    // Lane constants: load instruction c fills 16-byte position idx = lane +
+    // 64c of the slot, staged row srow (block srow >= 16 of the pair).  The
+    // slot is row-major with its chunks XOR-swizzled per row (chunk k of row
+    // r at position k ^ swz(r)), which spreads the rows one
+    // ds_read_b64_tr_b16 touches over all LDS banks; so position idx holds
+    // chunk (idx % CH) ^ swz(srow): columns n .. n+7, byte offset nbyte of
+    // its B row.  Columns past N read a valid chunk of the row instead; their
+    // products land in output columns >= N, which are never stored.
+    auto swz = [](int r) { return (2 * ((r >> 1) ^ (r >> 3))) & (CH - 1); };
     int srow[CPL], nbyte[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
         const int idx = lane + c * 64;
         srow[c] = idx / CH;
-        const int n = n0 + (idx % CH) * 8;
+        const int n = n0 + ((idx % CH) ^ swz(srow[c])) * 8;
         nbyte[c] = (n < a.N ? n : 0) * 2;
     }
+    // B operand reads: rows 8g + t/4 (lo) and +4 (hi), chunk 2j + (t & 3) / 2
+    // of the row, bytes 8 * (t & 1) of it; swz(r) is even, so the swizzle
+    // XORs the tile index j with swz(r) / 2.
+    const int h_lo  = swz(8 * g + (t >> 2)) >> 1;
+    const int h_hi  = swz(8 * g + (t >> 2) + 4) >> 1;
+    const int in_lo = (8 * g + (t >> 2)) * NT + ((t & 3) >> 1) * 8 + (t & 1) * 4;  // fp16 units
+    const int in_hi = in_lo + 4 * NT;
     // A operand: row t of block (first, g < 2) or (second, g >= 2), columns 8*(g&1) .. +7
     const int a_off = t * 32 + 16 * (g & 1);
     const int a_hi  = g >> 1;
@@ -384,11 +403,11 @@ __device__ __forceinline__ void bsr_record_body(const BsrArgs& a, _Float16* __re
     };
     auto multiply = [&](int d) {
         const f16x8 afv = __builtin_bit_cast(f16x8, af[d]);
-        const _Float16* rowp = slot(d) + (8 * g + (t >> 2)) * NT + 4 * (t & 3);
+        const _Float16* st = slot(d);
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const s16x4 lo = lds_read_tr16(rowp + 16 * j);
-            const s16x4 hi = lds_read_tr16(rowp + 4 * NT + 16 * j);
+            const s16x4 lo = lds_read_tr16(st + in_lo + (j ^ h_lo) * 16);
+            const s16x4 hi = lds_read_tr16(st + in_hi + (j ^ h_hi) * 16);
             const s16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afv, __builtin_bit_cast(f16x8, both),
                                                              acc[j], 0, 0, 0);
@@ -461,565 +480,471 @@ __global__ __launch_bounds__(256) void bsr_record_kernel(BsrArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Multi-row wave kernel: one wave = R consecutive block-rows x 16*J columns.
-// The wave walks the union of the R block-rows' (sorted) block-column lists
-// with R scalar cursors; every union pair's 32 B rows are loaded and staged
-// in LDS once and feed R MFMAs (one per block-row, zero A where a block-row
-// has no block at that column).  Neighbouring block-rows of banded and
-// block-diagonal matrices share most block-columns, so B traffic through the
-// CU and LDS falls by up to R without any workgroup barrier.
-//   - The R block-rows' blocks are contiguous in col_idx; when they total at
-//     most 64 they come in with one vector load and are merged in one
-//     segment.  Longer ones are taken block-row by block-row in chunks of 64
-//     (the other cursors empty).
-//   - The union cursor advances inside load_pair, so pairs are produced in
-//     order; loads are unconditional (exhausted cursors give masked loads of
-//     clamped valid addresses), as in the wave kernel.
+// Shared-panel kernel: a workgroup owns R consecutive block-rows (16R rows of
+// C) and NT = 16*J columns, and multiplies them by B one union block pair at
+// a time.
+//   1. Union of the R block-rows' block-column lists (contiguous in col_idx).
+//      Fast path, when every block-column lies within 64 of the smallest and
+//      there are at most 256 entries: each wave ORs a 64-bit mask per
+//      block-row with DPP and one barrier combines the waves.  Otherwise an
+//      LDS bitmap over all block-columns (up to kPanelMaxWords * 32) and an
+//      exclusive prefix of its words' popcounts rank every block-column.
+//   2. The union's slots go into lane-indexed registers (per slot: the
+//      block-column, and this wave's blocks there or -1), which the pipeline
+//      reads with v_readlane: a pair costs the scalar unit only its slot
+//      numbers, and the pipeline reads no LDS but the B stages.
+//   3. Slots are multiplied in pairs (two 16-deep blocks are one K = 32 step
+//      of v_mfma_f32_16x16x32_f16).  A pair's 32 B rows x NT columns are
+//      loaded once per workgroup straight into an LDS stage (buffer-to-LDS
+//      loads, XOR-swizzled against bank conflicts) and read by every wave
+//      with ds_read_b64_tr_b16; each wave loads the A operands of its own
+//      block-rows (an absent block has index -1 and reads as zeros through
+//      the buffer range check).  D stages in flight, one barrier per pair.
+//   4. The four waves form a WR x (4/WR) grid over the tile: a wave multiplies
+//      R/WR block-rows by J/(4/WR) 16-column tiles.
+// Lists that are not strictly ascending or hold block-columns outside the
+// matrix, and matrices wider than the bitmap, use the identity union (slot u =
+// entry u of the concatenated lists): correct for any BSR, at up to R times
+// the matrix-core work.
+//
+// What it buys, measured on MI355X (rocprofv3 counters, c4): the wave
+// kernel's four waves of a workgroup already share their B tiles through the
+// vector L1 -- both kernels make the same 263 K L2 read requests per launch
+// -- so the panel saves L1 accesses (0.66 M vs 1.44 M of 64 bytes) but pays
+// barriers, lockstep phases and LDS read bandwidth.  It is faster only on
+// wide B with long block-rows (N >= 256 and 24 - 64 blocks per block-row:
+// 1.03 - 1.31x, e.g. block-diagonal 512 at N = 512 12.6 -> 10.8 us), which is
+// where the launcher picks it; c3 and c4 stay on the wave kernel.
 // ---------------------------------------------------------------------------
-template <int R, int J, int D, bool VEC>
-struct MultirowWave {
-    static constexpr int NT  = 16 * J;
-    static constexpr int S   = NT + 16;
-    static constexpr int CH  = NT / 8;
-    static constexpr int CPL = 32 * CH / 64;
-    static constexpr int kNone = 0x7fffffff;
+constexpr int kPanelMaxWords = 256;  // union bitmap: up to 8192 block-columns (K <= 131072)
+constexpr int kPanelSlots    = 126;  // union slots per pass (two registers per lane, lane 127 free)
 
-    struct PairRegs {
-        f16x8 b[CPL];
-        f16x8 af[R];
-        bool  b_ok[CPL];
-        bool  a_ok[R];
-        bool  valid;  // wave-uniform: the pair holds at least one union element
-    };
-
-    const BsrArgs& a;
-    _Float16*      tile;
-    int            lane, g, t, n0;
-    f32x4          acc[R][J];
-    // Current segment: lanes [0, cnt) of ci hold col_idx[base + lane]; list r
-    // (block-row r) is lanes [cur[r], end[r]).
-    int            base, ci;
-    int            cur[R], end[R];
-
-    __device__ MultirowWave(const BsrArgs& args, _Float16* t_, int n0_) : a(args), tile(t_), n0(n0_) {
-        lane = threadIdx.x & 63;
-        g    = lane >> 4;
-        t    = lane & 15;
+__device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-#pragma unroll
-            for (int j = 0; j < J; ++j) acc[r][j] = f32x4(0.0f);
-        }
+    for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(v, d, 64);
+        if (lane >= d) v += u;
     }
+    return v;
+}
 
-    // Next union element: its block-column (-1 when the lists are exhausted)
-    // and, per block-row, its block index (-1 where the block-row has none).
-    __device__ void next_union(int& bc, int (&blk)[R]) {
-        int c[R];
-        int m = kNone;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int v = __builtin_amdgcn_readlane(ci, min(cur[r], 63));
-            c[r] = cur[r] < end[r] ? v : kNone;
-            m = min(m, c[r]);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const bool has = m != kNone && c[r] == m;
-            blk[r] = has ? base + cur[r] : -1;
-            cur[r] += has ? 1 : 0;
-        }
-        bc = m == kNone ? -1 : m;
-    }
+// OR of a 64-bit value over the 64 lanes of a wave (all lanes active): DPP
+// xor-1 and xor-2 inside quads, then half-row and row mirrors give every
+// lane its row's OR, and the four rows are combined from lanes 0, 16, 32, 48.
+__device__ __forceinline__ uint64_t wave_or64(uint64_t v) {
+    unsigned lo = static_cast<unsigned>(v), hi = static_cast<unsigned>(v >> 32);
+    lo |= __builtin_amdgcn_update_dpp(0u, lo, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    hi |= __builtin_amdgcn_update_dpp(0u, hi, 0xB1, 0xF, 0xF, false);
+    lo |= __builtin_amdgcn_update_dpp(0u, lo, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    hi |= __builtin_amdgcn_update_dpp(0u, hi, 0x4E, 0xF, 0xF, false);
+    lo |= __builtin_amdgcn_update_dpp(0u, lo, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    hi |= __builtin_amdgcn_update_dpp(0u, hi, 0x141, 0xF, 0xF, false);
+    lo |= __builtin_amdgcn_update_dpp(0u, lo, 0x140, 0xF, 0xF, false);  // row_mirror
+    hi |= __builtin_amdgcn_update_dpp(0u, hi, 0x140, 0xF, 0xF, false);
+    const unsigned rlo = __builtin_amdgcn_readlane(lo, 0) | __builtin_amdgcn_readlane(lo, 16) |
+                         __builtin_amdgcn_readlane(lo, 32) | __builtin_amdgcn_readlane(lo, 48);
+    const unsigned rhi = __builtin_amdgcn_readlane(hi, 0) | __builtin_amdgcn_readlane(hi, 16) |
+                         __builtin_amdgcn_readlane(hi, 32) | __builtin_amdgcn_readlane(hi, 48);
+    return (static_cast<uint64_t>(rhi) << 32) | rlo;
+}
 
-    __device__ void load_pair(PairRegs& rg) {
-        int bc0, bc1, blk0[R], blk1[R];
-        next_union(bc0, blk0);
-        next_union(bc1, blk1);
-        rg.valid = bc0 >= 0;
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            const int idx = lane + c * 64;
-            const int s   = idx / CH;
-            const int bc  = s < 16 ? bc0 : bc1;
-            const int k   = bc * 16 + (s & 15);
-            const int n   = n0 + (idx % CH) * 8;
-            const bool ok = bc >= 0 && k < a.K && n < a.N;
-            rg.b_ok[c] = ok;
-            if constexpr (VEC) {
-                const size_t off = ok ? static_cast<size_t>(k) * a.N + n : 0;
-                rg.b[c] = *reinterpret_cast<const f16x8*>(a.B + off);
-            } else {
-                const size_t row = ok ? static_cast<size_t>(k) * a.N : 0;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const bool in = ok && n + e < a.N;
-                    const _Float16 x = a.B[in ? row + n + e : 0];
-                    rg.b[c][e] = in ? x : static_cast<_Float16>(0.0f);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int blk = g < 2 ? blk0[r] : blk1[r];
-            rg.a_ok[r] = blk >= 0;
-            rg.af[r] = *reinterpret_cast<const f16x8*>(
-                a.vals + static_cast<size_t>(blk >= 0 ? blk : base) * 256 + t * 16 + 8 * (g & 1));
-        }
-    }
+__device__ __forceinline__ uint64_t below(int p) {  // bits 0 .. p-1, p in [0, 64)
+    return (1ull << p) - 1ull;
+}
 
-    __device__ void multiply(const PairRegs& rg) {
-        const f16x8 zero = f16x8(static_cast<_Float16>(0.0f));
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            const int idx = lane + c * 64;
-            *reinterpret_cast<f16x8*>(&tile[(idx / CH) * S + (idx % CH) * 8]) =
-                rg.b_ok[c] ? rg.b[c] : zero;
-        }
-        const _Float16* rowp = &tile[(8 * g + (t >> 2)) * S + 4 * (t & 3)];
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const s16x4 lo = lds_read_tr16(rowp + 16 * j);
-            const s16x4 hi = lds_read_tr16(rowp + 4 * S + 16 * j);
-            const s16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            const f16x8 bop = __builtin_bit_cast(f16x8, both);
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const f16x8 af = rg.a_ok[r] ? rg.af[r] : zero;
-                acc[r][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bop, acc[r][j], 0, 0, 0);
-            }
-        }
-    }
+template <int R, int J, int WR, int D>
+__device__ __forceinline__ void bsr_panel_body(const BsrArgs& a, _Float16* __restrict__ s0,
+                                               _Float16* __restrict__ s1,
+                                               _Float16* __restrict__ s2,
+                                               _Float16* __restrict__ s3,
+                                               uint32_t* __restrict__ s_bits,
+                                               int* __restrict__ s_pre, int* __restrict__ s_ucol,
+                                               int* __restrict__ s_blk,
+                                               uint64_t* __restrict__ s_mask,
+                                               int* __restrict__ s_misc) {
+    constexpr int WC  = 4 / WR;
+    constexpr int TR  = R / WR;          // block-rows per wave
+    constexpr int TC  = J / WC;          // 16-column tiles per wave
+    constexpr int NT  = 16 * J;          // columns per workgroup
+    constexpr int CH  = NT / 8;          // 16-byte chunks per staged B row
+    constexpr int CPT = 32 * CH / 256;   // chunks per thread per pair
+    constexpr int PER = CPT + TR;        // vector-memory instructions per thread per pair
+    static_assert(WR * WC == 4 && TR * WR == R && TC * WC == J, "wave grid");
+    static_assert(CPT >= 1 && CPT * 256 == 32 * CH, "whole chunks per thread");
+    static_assert(64 / CH <= 16, "a wave's chunks of one load stay inside one block");
+    static_assert(D == 2 || D == 4, "2 or 4 stages");
 
-    // Walks the union of the current segment's lists.  Every slot of the ring
-    // is refilled unconditionally after its turn, so each iteration issues
-    // the same loads and the wait before a multiply covers only that slot.
-    // The union comes out in order: once slot 0 holds no union element, no
-    // later pair does.
-    __device__ void run_segment(int base_, int cnt) {
-        base = base_;
-        ci = lane < cnt ? a.col_idx[base + lane] : 0;
-        PairRegs ring[D];
-#pragma unroll
-        for (int d = 0; d < D; ++d) load_pair(ring[d]);
-        while (ring[0].valid) {
-#pragma unroll
-            for (int d = 0; d < D; ++d) {
-                if (ring[d].valid) multiply(ring[d]);
-                load_pair(ring[d]);
-                // keep the slots' loads in issue order (the memory counter
-                // retires in order): a slot's wait then covers only its own
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-    }
-
-    __device__ void store(int br0) {
-        // D layout: lane holds rows 4*g + i, column t of each 16-column tile.
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int br = br0 + r;
-            if (br >= a.block_rows) break;
-#pragma unroll
-            for (int j = 0; j < J; ++j) {
-                const int col = n0 + 16 * j + t;
-                if (col >= a.N) continue;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int row = br * 16 + 4 * g + i;
-                    if (row < a.M) store_c(a.C + static_cast<size_t>(row) * a.N + col, acc[r][j][i]);
-                }
-            }
-        }
-    }
-};
-
-template <int R, int J, int D, bool VEC>
-__global__ __launch_bounds__(256) void bsr_multirow_kernel(BsrArgs a) {
-    constexpr int S = 16 * J + 16;
-    __shared__ __attribute__((aligned(16))) _Float16 s_b[4][32 * S];
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tid  = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g    = lane >> 4;
+    const int t    = lane & 15;
+    const int wr   = wave / WC;
+    const int wc   = wave % WC;
     int bx, by;
     wave_tile_of(a, bx, by);
-    const int br0 = (bx * 4 + wave) * R;
-    if (br0 >= a.block_rows) return;  // waves are independent: no barrier anywhere
-    MultirowWave<R, J, D, VEC> w(a, s_b[wave], by * 16 * J);
+    const int br0 = bx * R;
+    const int n0  = by * NT;
+    auto stage = [&](int d) -> _Float16* { return d == 0 ? s0 : d == 1 ? s1 : d == 2 ? s2 : s3; };
 
+    const __amdgpu_buffer_rsrc_t rec_b = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(a.B), static_cast<short>(a.N * 2), a.K, kBufWord3);
+    const __amdgpu_buffer_rsrc_t rec_a = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(a.vals), static_cast<short>(512), a.num_blocks, kBufWord3);
+
+    // Block-rows br0 .. br0+R-1 (those past the matrix are empty); their
+    // lists are contiguous in col_idx from e0.
     int rp[R + 1];
 #pragma unroll
     for (int r = 0; r <= R; ++r) rp[r] = a.row_ptr[min(br0 + r, a.block_rows)];
-    const int tot = rp[R] - rp[0];
-    if (tot <= 64) {
-        // the R block-rows' blocks are contiguous: one segment, all lists
+    const int e0 = rp[0];
+    const int T  = rp[R] - e0;
+    auto list_of = [&](int e) {  // block-row (0 .. R-1) of entry e0 + e
+        int r = 0;
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            w.cur[r] = rp[r] - rp[0];
-            w.end[r] = rp[r + 1] - rp[0];
+        for (int i = 1; i < R; ++i) r += (e0 + e >= rp[i]) ? 1 : 0;
+        return r;
+    };
+    auto list_start = [&](int e) {  // first entry of e0 + e's block-row (selects, no indexing)
+        int st = rp[0];
+#pragma unroll
+        for (int i = 1; i < R; ++i) st = (e0 + e >= rp[i]) ? rp[i] : st;
+        return st;
+    };
+    // Span of the block-columns from the lists' first and last entries.
+    int lo = 0x7fffffff, hi = -1;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (rp[r + 1] > rp[r]) {
+            lo = min(lo, a.col_idx[rp[r]]);
+            hi = max(hi, a.col_idx[rp[r + 1] - 1]);
         }
-        if (tot > 0) w.run_segment(rp[0], tot);
+    }
+    // Stage layout: row-major 32 x NT fp16, its 16-byte chunks XOR-swizzled
+    // per row (chunk c of row r sits at position c ^ swz(r)), which spreads
+    // the sixteen rows one ds_read_b64_tr_b16 touches over all banks (4
+    // conflict-free cycles instead of 16 with 32 banks).  A buffer-to-LDS load
+    // puts lane i's 16 bytes at a fixed position, so the swizzle picks which
+    // chunk each lane loads: load c of a pair fills position idx = 256c + tid,
+    // i.e. staged row srow, with chunk (idx % CH) ^ swz(srow): columns n ..
+    // n+7.  Rows 0-15 hold the pair's first block-column, 16-31 the second
+    // (the same half for a whole wave's load).  Columns past N read a valid
+    // chunk of the row instead; their products land in output columns >= N,
+    // which are never stored.
+    auto swz = [](int r) { return (2 * ((r >> 1) ^ (r >> 3))) & (CH - 1); };
+    int srow[CPT], nbyte[CPT];
+    bool second[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int idx = c * 256 + tid;
+        srow[c]   = idx / CH;
+        second[c] = __builtin_amdgcn_readfirstlane(srow[c] >> 4) != 0;
+        const int n = n0 + ((idx % CH) ^ swz(srow[c])) * 8;
+        nbyte[c] = (n < a.N ? n : 0) * 2;
+    }
+
+    // A operand: row t of the pair's block g >> 1, columns 8 * (g & 1) .. +7
+    const int a_off = t * 32 + 16 * (g & 1);
+    // B operand reads: lane (g, t) addresses rows 8g + t/4 (lo) and +4 (hi),
+    // chunk 2 * tile + (t & 3) / 2 of the row, bytes 8 * (t & 1) of it; with
+    // swz(r) even, the swizzle XORs the tile index with swz(r) / 2.
+    const int row_lo = 8 * g + (t >> 2);
+    const int h_lo   = swz(row_lo) >> 1;
+    const int h_hi   = swz(row_lo + 4) >> 1;
+    const int in_lo  = row_lo * NT + ((t & 3) >> 1) * 8 + (t & 1) * 4;  // fp16 units
+    const int in_hi  = in_lo + 4 * NT;
+
+    f32x4 acc[TR][TC];
+#pragma unroll
+    for (int i = 0; i < TR; ++i) {
+#pragma unroll
+        for (int j = 0; j < TC; ++j) acc[i][j] = f32x4(0.0f);
+    }
+    u32x4 af[D][TR];
+
+    int off_lo[TC], off_hi[TC];  // per tile: this lane's B operand addresses in a stage
+#pragma unroll
+    for (int j = 0; j < TC; ++j) {
+        off_lo[j] = in_lo + ((wc * TC + j) ^ h_lo) * 16;
+        off_hi[j] = in_hi + ((wc * TC + j) ^ h_hi) * 16;
+    }
+    auto compute = [&](int d) {
+        const _Float16* st = stage(d);
+#pragma unroll
+        for (int j = 0; j < TC; ++j) {
+            const s16x4 lo4 = lds_read_tr16(st + off_lo[j]);
+            const s16x4 hi4 = lds_read_tr16(st + off_hi[j]);
+            const s16x8 both = {lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+            const f16x8 bop = __builtin_bit_cast(f16x8, both);
+#pragma unroll
+            for (int i = 0; i < TR; ++i) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(f16x8, af[d][i]), bop, acc[i][j], 0, 0, 0);
+            }
+        }
+    };
+
+    // This thread's entry (the fast path needs at most one per thread).
+    const int  x    = tid < T ? a.col_idx[e0 + tid] : 0;
+    const int  xp   = tid < T && tid > 0 ? a.col_idx[e0 + tid - 1] : -1;
+    const int  my_r = list_of(tid);
+    // ---- 1. union of the R lists (fast path: DPP masks and one barrier;
+    // otherwise the LDS bitmap and its word prefix; identity union for lists
+    // that fail the checks or matrices wider than the bitmap).
+    const bool fast_shape = T > 0 && T <= 256 && lo >= 0 && hi - lo < 64;
+    const int  nwords     = (a.block_cols + 31) >> 5;
+    const bool fits       = nwords <= kPanelMaxWords;
+    bool bad = false;
+    if (fast_shape) {
+        const bool ok = tid >= T || (static_cast<unsigned>(x) < static_cast<unsigned>(a.block_cols) &&
+                                     x >= lo && x - lo < 64 &&
+                                     (e0 + tid == list_start(tid) || xp < x));
+        const uint64_t bit = (tid < T && ok) ? (1ull << (x - lo)) : 0ull;
+        uint64_t wm[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) wm[r] = wave_or64(my_r == r ? bit : 0ull);
+        const bool wbad = __ballot(!ok) != 0;
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) s_mask[wave * R + r] = wm[r];
+            s_misc[4 + wave] = wbad ? 1 : 0;
+        }
     } else {
-        // block-row by block-row in chunks of 64 blocks (other lists empty)
+        if (fits) {
+            for (int w = tid; w < nwords; w += 256) s_bits[w] = 0u;
+        }
+        if (tid == 0) s_misc[0] = fits ? 0 : 1;  // 1: identity union
+    }
+    for (int i = tid; i < kPanelSlots * R; i += 256) s_blk[i] = -1;
+    __syncthreads();
+    uint64_t rmask[R];  // fast path: block-row r's block-columns, bit = column - lo
+    if (fast_shape) {
+        bad = (s_misc[4] | s_misc[5] | s_misc[6] | s_misc[7]) != 0;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            for (int c0 = rp[r]; c0 < rp[r + 1]; c0 += 64) {
-                const int cnt = min(64, rp[r + 1] - c0);
-#pragma unroll
-                for (int q = 0; q < R; ++q) {
-                    w.cur[q] = 0;
-                    w.end[q] = q == r ? cnt : 0;
-                }
-                w.run_segment(c0, cnt);
-            }
+            rmask[r] = s_mask[r] | s_mask[R + r] | s_mask[2 * R + r] | s_mask[3 * R + r];
         }
     }
-    w.store(br0);
-}
-
-// ---------------------------------------------------------------------------
-// Split-K wave kernel: a workgroup of 4 waves owns one block-row x 16*J
-// columns; wave w multiplies the block pairs p = w, w+4, w+8, ... of the
-// block-row (pairs of consecutive blocks, as in the wave kernel), so each
-// wave's dependent chain is a quarter as long and four times as many waves
-// are in flight.  The four partial tiles are summed through LDS after one
-// workgroup barrier; wave w adds rows 4w .. 4w+3 of the tile and stores them.
-// ---------------------------------------------------------------------------
-template <int J, int D, bool VEC>
-__global__ __launch_bounds__(256) void bsr_splitk_kernel(BsrArgs a) {
-    constexpr int NT  = 16 * J;
-    constexpr int S   = NT + 16;
-    constexpr int CH  = NT / 8;
-    constexpr int CPL = 32 * CH / 64;
-    __shared__ __attribute__((aligned(16))) _Float16 s_b[4][32 * S];
-    __shared__ float s_part[4][16][NT + 1];
-
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int g    = lane >> 4;
-    const int t    = lane & 15;
-    int bx, by;
-    wave_tile_of(a, bx, by);
-    const int br = bx;  // grid = block_rows x column tiles: always a valid block-row
-    const int n0 = by * NT;
-    _Float16* tile = s_b[wave];
-    const int bs = a.row_ptr[br];
-    const int be = a.row_ptr[br + 1];
-
-    f32x4 acc[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) acc[j] = f32x4(0.0f);
-
-    struct PairRegs {
-        f16x8 b[CPL];
-        f16x8 af;
-        bool  b_ok[CPL];
-        bool  a_ok;
-    };
-    // pair q of the chunk = blocks 2q and 2q+1 of chunk ci (which starts at block base)
-    auto load_pair = [&](int base, int q, int cnt, int ci, PairRegs& r) {
-        const int p = min(2 * q, cnt - 1);  // clamped past the end: masked below
-        const bool live = 2 * q < cnt;
-        const bool two = live && p + 1 < cnt;
-        const int bc0 = __builtin_amdgcn_readlane(ci, p);
-        const int bc1 = __builtin_amdgcn_readlane(ci, two ? p + 1 : p);
-        const int blk = base + p;
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            const int idx = lane + c * 64;
-            const int s   = idx / CH;
-            const int k   = (s < 16 ? bc0 : bc1) * 16 + (s & 15);
-            const int n   = n0 + (idx % CH) * 8;
-            const bool ok = live && (s < 16 || two) && k < a.K && n < a.N;
-            r.b_ok[c] = ok;
-            if constexpr (VEC) {
-                const size_t off = ok ? static_cast<size_t>(k) * a.N + n : 0;
-                r.b[c] = *reinterpret_cast<const f16x8*>(a.B + off);
-            } else {
-                const size_t row = ok ? static_cast<size_t>(k) * a.N : 0;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const bool in = ok && n + e < a.N;
-                    const _Float16 x = a.B[in ? row + n + e : 0];
-                    r.b[c][e] = in ? x : static_cast<_Float16>(0.0f);
-                }
+    const bool use_fast = fast_shape && !bad;
+    bool identity = fast_shape ? bad : false;
+    if (!fast_shape) {
+        for (int e = tid; e < T; e += 256) {
+            const int xe = e < 256 ? x : a.col_idx[e0 + e];
+            const bool wrong = static_cast<unsigned>(xe) >= static_cast<unsigned>(a.block_cols) ||
+                               (e0 + e != list_start(e) && a.col_idx[e0 + e - 1] >= xe);
+            if (wrong) {
+                s_misc[0] = 1;  // every writer stores 1
+            } else if (fits) {
+                atomicOr(&s_bits[xe >> 5], 1u << (xe & 31));
             }
-        }
-        r.a_ok = live && (g < 2 || two);
-        r.af = *reinterpret_cast<const f16x8*>(
-            a.vals + static_cast<size_t>(blk + (r.a_ok ? (g >> 1) : 0)) * 256 + t * 16 +
-            8 * (g & 1));
-    };
-    auto multiply = [&](const PairRegs& r) {
-        const f16x8 zero = f16x8(static_cast<_Float16>(0.0f));
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            const int idx = lane + c * 64;
-            *reinterpret_cast<f16x8*>(&tile[(idx / CH) * S + (idx % CH) * 8]) =
-                r.b_ok[c] ? r.b[c] : zero;
-        }
-        const f16x8 af = r.a_ok ? r.af : zero;
-        const _Float16* rowp = &tile[(8 * g + (t >> 2)) * S + 4 * (t & 3)];
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const s16x4 lo = lds_read_tr16(rowp + 16 * j);
-            const s16x4 hi = lds_read_tr16(rowp + 4 * S + 16 * j);
-            const s16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, __builtin_bit_cast(f16x8, both),
-                                                             acc[j], 0, 0, 0);
-        }
-    };
-
-    for (int c0 = bs; c0 < be; c0 += 64) {
-        const int cnt = min(64, be - c0);
-        const int np  = (cnt + 1) >> 1;
-        const int mine = np > wave ? (np - wave + 3) >> 2 : 0;  // pairs wave, wave+4, ...
-        if (mine == 0) continue;
-        const int ci = lane < cnt ? a.col_idx[c0 + lane] : 0;
-        PairRegs ring[D];
-#pragma unroll
-        for (int d = 0; d < D; ++d) load_pair(c0, wave + 4 * d, cnt, ci, ring[d]);
-        int i0 = 0;
-        for (; i0 + 2 * D <= mine; i0 += D) {
-#pragma unroll
-            for (int d = 0; d < D; ++d) {
-                multiply(ring[d]);
-                load_pair(c0, wave + 4 * (i0 + d + D), cnt, ci, ring[d]);
-            }
-        }
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            if (i0 + d < mine) {
-                multiply(ring[d]);
-                if (i0 + d + D < mine) load_pair(c0, wave + 4 * (i0 + d + D), cnt, ci, ring[d]);
-            }
-        }
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            if (i0 + D + d < mine) multiply(ring[d]);
-        }
-    }
-
-    // Partial tiles -> LDS (lane holds rows 4g+i, column 16j+t), one barrier,
-    // then wave w sums rows 4w .. 4w+3 over the four partials.
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s_part[wave][4 * g + i][16 * j + t] = acc[j][i];
-    }
-    __syncthreads();
-    for (int e = lane; e < 4 * NT; e += 64) {
-        const int lr  = 4 * wave + e / NT;
-        const int col = e % NT;
-        const float v = s_part[0][lr][col] + s_part[1][lr][col] + s_part[2][lr][col] +
-                        s_part[3][lr][col];
-        const int row = br * 16 + lr;
-        if (row < a.M && n0 + col < a.N) store_c(a.C + static_cast<size_t>(row) * a.N + n0 + col, v);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Row-group kernel.
-//
-// A workgroup of RG waves owns RG consecutive block-rows (one per wave) and
-// a tile of NT = 16*J columns.  It first ORs the block-columns of its
-// block-rows into an LDS bitmap, then walks that union in ascending pairs
-// (bc0, bc1): each pair's 32 B rows x NT columns are loaded once into LDS,
-// row-major, with 16-byte loads, and every wave that owns a block at bc0 or
-// bc1 multiplies it by the staged rows.  Block-rows with shared block-columns
-// (banded, block-diagonal) therefore read each B tile once per workgroup
-// instead of once per block-row.
-//
-// The B operand is read back with ds_read_b64_tr_b16, which returns the
-// transpose of a 4 (k) x 16 (n) fp16 tile to each 16-lane block: lane s of the
-// block addresses row 8g + s/4 (+4 for the second read), columns 4*(s%4) ..
-// +3, and lane t receives rows 8g .. 8g+3 (8g+4 .. 8g+7) of column t, i.e. the
-// K-contiguous B operand of v_mfma_f32_16x16x32_f16.
-//
-// Pairs are processed in batches of P: all B tiles and A operands of a batch
-// are requested into registers before any is used, then stored to P LDS
-// tiles, so a batch costs one memory latency instead of one per pair.
-// ---------------------------------------------------------------------------
-constexpr int kMaxUnionWords = 2048;  // union bitmap of up to 65536 block-columns
-
-template <int RG, int J, int P>
-__global__ __launch_bounds__(RG * 64) void bsr_rowgroup_kernel(BsrArgs a) {
-    constexpr int NT          = 16 * J;      // columns per workgroup
-    constexpr int S           = NT + 16;     // LDS row stride in fp16: S/2 = 8 (mod 32) banks
-    constexpr int CH          = NT / 8;      // 16-byte chunks per staged row
-    constexpr int TILE_CHUNKS = 32 * CH;
-    constexpr int THREADS     = RG * 64;
-    constexpr int CPT         = (TILE_CHUNKS + THREADS - 1) / THREADS;  // chunks per thread
-
-    // Dynamic LDS: P tiles of 32 x S fp16 (one per pair of a batch), then the
-    // union bitmap sized to the matrix's block-columns.
-    extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
-    _Float16 (*s_b)[32 * S] = reinterpret_cast<_Float16 (*)[32 * S]>(s_dyn);
-    uint32_t* s_bits = reinterpret_cast<uint32_t*>(s_dyn + sizeof(_Float16) * P * 32 * S);
-
-    const int tid    = threadIdx.x;
-    const int lane   = tid & 63;
-    const int wave   = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g      = lane >> 4;
-    const int t      = lane & 15;
-    const int br     = blockIdx.x * RG + wave;
-    const int n0     = blockIdx.y * NT;
-    const int nwords = (a.block_cols + 31) / 32;
-
-    int bs = 0, be = 0;
-    if (br < a.block_rows) {
-        bs = a.row_ptr[br];
-        be = a.row_ptr[br + 1];
-    }
-    // this wave's own block list, 64 block-columns per register chunk; the
-    // first chunk also feeds the union below
-    int ptr = bs, chunk = bs;
-    int my_col = (bs + lane < be) ? a.col_idx[bs + lane] : 0x7fffffff;
-
-    // ---- union of the group's block-columns
-    for (int i = tid; i < nwords; i += THREADS) s_bits[i] = 0u;
-    __syncthreads();
-    for (int b = bs + lane; b < be; b += 64) {
-        const int bc = b - bs < 64 ? my_col : a.col_idx[b];
-        if (static_cast<unsigned>(bc) < static_cast<unsigned>(a.block_cols)) {
-            atomicOr(&s_bits[bc >> 5], 1u << (bc & 31));
-        }
-    }
-    __syncthreads();
-
-    auto current_col = [&]() -> int {
-        if (ptr >= be) return 0x7fffffff;
-        if (ptr - chunk >= 64) {
-            chunk = ptr;
-            my_col = (ptr + lane < be) ? a.col_idx[ptr + lane] : 0x7fffffff;
-        }
-        return __builtin_amdgcn_readlane(my_col, ptr - chunk);
-    };
-
-    // ---- cursor over the union (identical in every thread)
-    int cw = -1;
-    uint32_t cbits = 0u;
-    auto next_col = [&]() -> int {
-        while (cbits == 0u) {
-            if (++cw >= nwords) return -1;
-            cbits = s_bits[cw];
-        }
-        const int b = __builtin_ctz(cbits);
-        cbits &= cbits - 1u;
-        return cw * 32 + b;
-    };
-
-    auto load_tile = [&](int bc0, int bc1, f16x8 (&r)[CPT]) {
-#pragma unroll
-        for (int c = 0; c < CPT; ++c) {
-            const int idx = tid + c * THREADS;
-            f16x8 v = f16x8(static_cast<_Float16>(0.0f));
-            if (idx < TILE_CHUNKS) {
-                const int s  = idx / CH;
-                const int bc = s < 16 ? bc0 : bc1;
-                const int k  = bc * 16 + (s & 15);
-                const int n  = n0 + (idx % CH) * 8;
-                if (bc >= 0 && k < a.K && n < a.N) {
-                    const _Float16* src = a.B + static_cast<size_t>(k) * a.N + n;
-                    if (a.b_vec_ok && n + 8 <= a.N) {
-                        v = *reinterpret_cast<const f16x8*>(src);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            if (n + e < a.N) v[e] = src[e];
-                        }
-                    }
-                }
-            }
-            r[c] = v;
-        }
-    };
-    auto store_tile = [&](int buf, const f16x8 (&r)[CPT]) {
-#pragma unroll
-        for (int c = 0; c < CPT; ++c) {
-            const int idx = tid + c * THREADS;
-            if (idx < TILE_CHUNKS) {
-                *reinterpret_cast<f16x8*>(&s_b[buf][(idx / CH) * S + (idx % CH) * 8]) = r[c];
-            }
-        }
-    };
-    // A operand of this wave for the pair; consumes the wave's matching blocks.
-    auto load_a = [&](int bc0, int bc1, bool& any) -> f16x8 {
-        int blk0 = -1, blk1 = -1;
-        if (current_col() == bc0) blk0 = ptr++;
-        if (bc1 >= 0 && current_col() == bc1) blk1 = ptr++;
-        any = blk0 >= 0 || blk1 >= 0;
-        const int blk = g < 2 ? blk0 : blk1;
-        f16x8 af = f16x8(static_cast<_Float16>(0.0f));
-        if (blk >= 0) {
-            af = *reinterpret_cast<const f16x8*>(a.vals + static_cast<size_t>(blk) * 256 + t * 16 +
-                                                 8 * (g & 1));
-        }
-        return af;
-    };
-
-    f32x4 acc[J];
-#pragma unroll
-    for (int j = 0; j < J; ++j) acc[j] = f32x4(0.0f);
-
-    // Batches of up to P pairs: every B tile and A operand of a batch is
-    // requested before any is used, so a batch costs one memory latency.
-    while (true) {
-        int bcl[2 * P];
-        int npairs = 0;
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-            bcl[2 * p]     = next_col();
-            bcl[2 * p + 1] = bcl[2 * p] >= 0 ? next_col() : -1;
-            npairs += bcl[2 * p] >= 0 ? 1 : 0;
-        }
-        if (npairs == 0) break;  // uniform across the workgroup
-
-        f16x8 treg[P][CPT];
-        f16x8 af[P];
-        bool  any[P];
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-            any[p] = false;
-            af[p]  = f16x8(static_cast<_Float16>(0.0f));
-            if (p < npairs) {
-                load_tile(bcl[2 * p], bcl[2 * p + 1], treg[p]);
-                af[p] = load_a(bcl[2 * p], bcl[2 * p + 1], any[p]);
-            }
-        }
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-            if (p < npairs) store_tile(p, treg[p]);
         }
         __syncthreads();
+        identity = s_misc[0] != 0;
+        if (!identity) {
+            if (wave == 0) {  // lane l: words 4l .. 4l+3 (nwords <= 256)
+                int pc[4], sum = 0;
 #pragma unroll
-        for (int p = 0; p < P; ++p) {
-            if (p < npairs && any[p]) {
-                const _Float16* rowp = &s_b[p][(8 * g + (t >> 2)) * S + 4 * (t & 3)];
-#pragma unroll
-                for (int j = 0; j < J; ++j) {
-                    const s16x4 lo = lds_read_tr16(rowp + 16 * j);
-                    const s16x4 hi = lds_read_tr16(rowp + 4 * S + 16 * j);
-                    const s16x8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        af[p], __builtin_bit_cast(f16x8, both), acc[j], 0, 0, 0);
+                for (int k = 0; k < 4; ++k) {
+                    const int w = 4 * lane + k;
+                    pc[k] = w < nwords ? __builtin_popcount(s_bits[w]) : 0;
+                    sum += pc[k];
                 }
+                const int incl = wave_inclusive_scan(sum, lane);
+                int run = incl - sum;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if (4 * lane + k < nwords) s_pre[4 * lane + k] = run;
+                    run += pc[k];
+                }
+                if (lane == 63) s_misc[1] = incl;
+            }
+            __syncthreads();
+        }
+    }
+    uint64_t umask = 0ull;
+    if (use_fast) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) umask |= rmask[r];
+    }
+    const int U = use_fast ? __builtin_popcountll(umask) : (identity ? T : s_misc[1]);
+    // This wave's block-rows wr*TR .. wr*TR+TR-1: first entries and masks,
+    // picked with selects (a runtime index into rp / rmask would put the
+    // arrays in scratch memory).
+    int      my_rp[TR];
+    uint64_t my_mask[TR];
+#pragma unroll
+    for (int i = 0; i < TR; ++i) {
+        my_rp[i]   = 0;
+        my_mask[i] = 0ull;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (r == wr * TR + i) {
+                my_rp[i] = rp[r];
+                if (use_fast) my_mask[i] = rmask[r];
             }
         }
-        if (npairs < P) break;
-        __syncthreads();  // the next batch overwrites the tiles
     }
 
-    if (br < a.block_rows) {
+    // ---- 2. the pass's slot tables in registers: lane l of tcol[k] holds the
+    // block-column of union slot 64k + l (-1 past the pass's end), lane l of
+    // tblk[i][k] the block of this wave's block-row i at that slot (-1 where
+    // it has none).  The pipeline reads them with v_readlane (a vector
+    // instruction), so a pair costs the scalar unit only its slot numbers and
+    // reads no LDS but the B stages.  Lane 63 of the last table always holds
+    // -1 (a pass has at most kPanelSlots <= 126 slots): slot numbers are
+    // clamped to it, so the zero pairs past the end need no test.
+    int tcol[2], tblk[TR][2];
+    // Pipeline over a pass of uc slots: pair q (slots 2q, 2q+1) lives in
+    // stage q % D.  Before pair q is read, each thread waits until its own
+    // loads of pair q have landed (loads retire in issue order, so the D - 2
+    // later pairs' loads may stay outstanding) and the barrier makes every
+    // thread's share visible.  The barrier is a bare s_barrier:
+    // __syncthreads' release fence would also wait for the later pairs'
+    // buffer-to-LDS writes, draining the ring at every pair.  A wave reaches
+    // it with its LDS reads of pair q - 1 complete (the matrix-core
+    // instructions consumed them), and the stage refilled right after it held
+    // pair q - 1.  Every issue is unconditional: pairs past the last one read
+    // -1 and load zeros (out of range, no memory traffic), so the loads in
+    // flight are the same on every path and the compiler's own wait counts
+    // stay exact.
+    auto pipeline = [&](int uc, auto two_tables) {
+        constexpr bool TWO = decltype(two_tables)::value;
+        auto pick = [&](const int (&v)[2], int u) -> int {
+            if constexpr (TWO) {
+                const int uu = min(u, 127);
+                return uu < 64 ? __builtin_amdgcn_readlane(v[0], uu)
+                               : __builtin_amdgcn_readlane(v[1], uu - 64);
+            } else {
+                return __builtin_amdgcn_readlane(v[0], min(u, 63));
+            }
+        };
+        auto issue = [&](int d, int q) {
+            _Float16* dst = stage(d);
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int col = n0 + 16 * j + t;
+            for (int c = 0; c < CPT; ++c) {
+                const int bc = pick(tcol, 2 * q + (second[c] ? 1 : 0));  // -1: rows -16..-1, zeros
+                sbuf_load_lds(rec_b, (spmm_lds_ptr)(dst + (c * 256 + wave * 64) * 8), 16,
+                              bc * 16 + (srow[c] & 15), nbyte[c], 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < TR; ++i) {
+                const int b0 = pick(tblk[i], 2 * q);
+                const int b1 = pick(tblk[i], 2 * q + 1);
+                af[d][i] = sbuf_load_u32x4_dev(rec_a, (g >> 1) ? b1 : b0, a_off);
+            }
+        };
+        const int npairs = (uc + 1) >> 1;
+#pragma unroll
+        for (int d = 0; d < D - 1; ++d) issue(d, d);
+        const int rounds = (npairs + D - 1) / D * D;
+        for (int q0 = 0; q0 < rounds; q0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                wait_vmcnt<(D - 2) * PER>();
+                lds_barrier();
+                issue((d + D - 1) % D, q0 + d + D - 1);
+                if (q0 + d < npairs) compute(d);
+            }
+        }
+        wait_vmcnt<0>();  // the zero loads of the pairs past the end
+    };
+
+    if (use_fast) {
+        // Lane p stands for block-column lo + p: if it is in the union, its
+        // slot is the number of union columns below it, and ds_permute pushes
+        // its table entries to that lane (lanes outside the union push to lane
+        // 63, which is at or past U and is reset to -1).
+        const bool in_u = ((umask >> lane) & 1ull) != 0;
+        const int  addr = (in_u ? __builtin_popcountll(umask & below(lane)) : 63) * 4;
+        const int  col  = __builtin_amdgcn_ds_permute(addr, lo + lane);
+        tcol[0] = lane < U ? col : -1;
+        tcol[1] = -1;
+#pragma unroll
+        for (int i = 0; i < TR; ++i) {
+            const bool has = ((my_mask[i] >> lane) & 1ull) != 0;
+            const int blk = has ? my_rp[i] + __builtin_popcountll(my_mask[i] & below(lane)) : -1;
+            const int got = __builtin_amdgcn_ds_permute(addr, blk);
+            tblk[i][0] = lane < U ? got : -1;
+            tblk[i][1] = -1;
+        }
+        if (U <= 63) {
+            pipeline(U, std::integral_constant<bool, false>());
+        } else {
+            pipeline(U, std::integral_constant<bool, true>());
+        }
+    } else {
+        for (int u0 = 0; u0 < U; u0 += kPanelSlots) {
+            const int uc = min(kPanelSlots, U - u0);
+            if (u0 > 0) {  // the first pass's table was cleared before the union
+                for (int i = tid; i < uc * R; i += 256) s_blk[i] = -1;
+                __syncthreads();
+            }
+            for (int e = tid; e < T; e += 256) {
+                const int xe = e < 256 ? x : a.col_idx[e0 + e];
+                int u = e - u0;
+                if (!identity) {
+                    u = s_pre[xe >> 5] +
+                        __builtin_popcount(s_bits[xe >> 5] & ((1u << (xe & 31)) - 1u)) - u0;
+                }
+                if (u >= 0 && u < uc) {
+                    s_blk[u * R + list_of(e)] = e0 + e;
+                    s_ucol[u] = xe;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int u = 64 * k + lane;
+                tcol[k] = u < uc ? s_ucol[u] : -1;
+#pragma unroll
+                for (int i = 0; i < TR; ++i) tblk[i][k] = u < uc ? s_blk[u * R + wr * TR + i] : -1;
+            }
+            if (uc <= 63) {
+                pipeline(uc, std::integral_constant<bool, false>());
+            } else {
+                pipeline(uc, std::integral_constant<bool, true>());
+            }
+            __syncthreads();  // the next pass rewrites the tables and the stages
+        }
+    }
+
+
+
+    // D layout: lane holds rows 4*g + i, column t of each 16-column tile.
+#pragma unroll
+    for (int i = 0; i < TR; ++i) {
+        const int br = br0 + wr * TR + i;
+#pragma unroll
+        for (int j = 0; j < TC; ++j) {
+            const int col = n0 + (wc * TC + j) * 16 + t;
             if (col >= a.N) continue;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = br * 16 + 4 * g + i;
-                if (row < a.M) store_c(a.C + static_cast<size_t>(row) * a.N + col, acc[j][i]);
+            for (int k = 0; k < 4; ++k) {
+                const int row = br * 16 + 4 * g + k;
+                if (row < a.M) store_c(a.C + static_cast<size_t>(row) * a.N + col, acc[i][j][k]);
             }
         }
     }
+}
+
+// The stages and tables are separate LDS objects passed as restrict pointers
+// (as in the record kernel): the wait-count pass then sees that reading one
+// stage does not depend on buffer-to-LDS writes still going into another.
+template <int R, int J, int WR, int D>
+__global__ __launch_bounds__(256) void bsr_panel_kernel(BsrArgs a) {
+    constexpr int TILE = 32 * 16 * J;
+    __shared__ __attribute__((aligned(16))) _Float16 s_b0[TILE];
+    __shared__ __attribute__((aligned(16))) _Float16 s_b1[TILE];
+    __shared__ __attribute__((aligned(16))) _Float16 s_b2[D >= 3 ? TILE : 8];
+    __shared__ __attribute__((aligned(16))) _Float16 s_b3[D >= 4 ? TILE : 8];
+    __shared__ uint32_t s_bits[kPanelMaxWords];
+    __shared__ int s_pre[kPanelMaxWords];
+    __shared__ int s_ucol[kPanelSlots];
+    __shared__ int s_blk[kPanelSlots * R];
+    __shared__ uint64_t s_mask[4 * R];
+    __shared__ int s_misc[8];
+    bsr_panel_body<R, J, WR, D>(a, s_b0, s_b1, s_b2, s_b3, s_bits, s_pre, s_ucol, s_blk, s_mask,
+                                s_misc);
 }
 
 Error fail(int status, std::string msg) { return Error{status, std::move(msg)}; }
@@ -1065,71 +990,24 @@ hipError_t dispatch_wave(int depth, bool pointer_addressing, const BsrArgs& args
                                     : run_wave<J, 4>(args, stream, pointer_addressing));
 }
 
-template <int R, int J, int D>
-hipError_t run_multirow(BsrArgs args, hipStream_t stream) {
+template <int R, int J, int WR, int D>
+hipError_t run_panel(BsrArgs args, hipStream_t stream) {
     args.tiles_n = ceil_div(args.N, 16 * J);
-    const long total = static_cast<long>(ceil_div(args.block_rows, 4 * R)) * args.tiles_n;
+    const long total = static_cast<long>(ceil_div(args.block_rows, R)) * args.tiles_n;
     if (total > 0x7fffffffL) return hipErrorInvalidConfiguration;
     args.wg_total = static_cast<int>(total);
-    dim3 grid(args.wg_total);
-    if (args.b_vec_ok) {
-        hipLaunchKernelGGL((bsr_multirow_kernel<R, J, D, true>), grid, dim3(256), 0, stream, args);
-    } else {
-        hipLaunchKernelGGL((bsr_multirow_kernel<R, J, D, false>), grid, dim3(256), 0, stream, args);
-    }
+    hipLaunchKernelGGL((bsr_panel_kernel<R, J, WR, D>), dim3(args.wg_total), dim3(256), 0, stream,
+                       args);
     return hipGetLastError();
 }
 
-template <int J, int D>
-hipError_t run_splitk(BsrArgs args, hipStream_t stream) {
-    args.tiles_n = ceil_div(args.N, 16 * J);
-    const long total = static_cast<long>(args.block_rows) * args.tiles_n;
-    if (total > 0x7fffffffL) return hipErrorInvalidConfiguration;
-    args.wg_total = static_cast<int>(total);
-    dim3 grid(args.wg_total);
-    if (args.b_vec_ok) {
-        hipLaunchKernelGGL((bsr_splitk_kernel<J, D, true>), grid, dim3(256), 0, stream, args);
-    } else {
-        hipLaunchKernelGGL((bsr_splitk_kernel<J, D, false>), grid, dim3(256), 0, stream, args);
-    }
-    return hipGetLastError();
-}
-
-hipError_t dispatch_splitk(int j, int depth, const BsrArgs& args, hipStream_t stream) {
-    if (j == 1) return depth == 1 ? run_splitk<1, 1>(args, stream) : run_splitk<1, 2>(args, stream);
-    if (j == 2) return depth == 1 ? run_splitk<2, 1>(args, stream) : run_splitk<2, 2>(args, stream);
-    return depth == 1 ? run_splitk<4, 1>(args, stream) : run_splitk<4, 2>(args, stream);
-}
-
-template <int R>
-hipError_t dispatch_multirow(int j, int depth, const BsrArgs& args, hipStream_t stream) {
-    if (j == 1) return depth == 1 ? run_multirow<R, 1, 1>(args, stream) : run_multirow<R, 1, 2>(args, stream);
-    if (j == 2) return depth == 1 ? run_multirow<R, 2, 1>(args, stream) : run_multirow<R, 2, 2>(args, stream);
-    return depth == 1 ? run_multirow<R, 4, 1>(args, stream) : run_multirow<R, 4, 2>(args, stream);
-}
-
-template <int RG, int J>
-hipError_t run_rowgroup(const BsrArgs& args, hipStream_t stream) {
-    dim3 grid(ceil_div(args.block_rows, RG), ceil_div(args.N, 16 * J));
-    // Batch of up to 8 pairs (16 block-columns: one diagonal block of c4, a
-    // whole banded row group of c3), fewer when each thread stages several
-    // 16-byte chunks per tile, to bound the staging registers (P * CPT <= 8).
-    constexpr int CPT = (32 * 2 * J + RG * 64 - 1) / (RG * 64);
-    constexpr int P = (8 / CPT) < 2 ? 2 : 8 / CPT;
-    constexpr size_t tiles_bytes = sizeof(_Float16) * P * 32 * (16 * J + 16);
-    const size_t lds = tiles_bytes + sizeof(uint32_t) * ((args.block_cols + 31) / 32);
-    hipLaunchKernelGGL((bsr_rowgroup_kernel<RG, J, P>), grid, dim3(RG * 64), lds, stream, args);
-    return hipGetLastError();
-}
-
-template <int RG>
-hipError_t dispatch_rowgroup(int j, const BsrArgs& args, hipStream_t stream) {
-    switch (j) {
-        case 1: return run_rowgroup<RG, 1>(args, stream);
-        case 2: return run_rowgroup<RG, 2>(args, stream);
-        case 8: return run_rowgroup<RG, 8>(args, stream);
-        default: return run_rowgroup<RG, 4>(args, stream);
-    }
+// Panel shapes: R block-rows x 16J columns per workgroup, each wave four
+// 16-column tiles (waves 4 x 1 for J = 4, 2 x 2 for J = 8).
+// Stages in flight: 2 or 4.
+template <int R, int J>
+hipError_t dispatch_panel(int depth, const BsrArgs& args, hipStream_t stream) {
+    constexpr int WR = J == 4 ? 4 : 2;
+    return depth <= 2 ? run_panel<R, J, WR, 2>(args, stream) : run_panel<R, J, WR, 4>(args, stream);
 }
 
 }  // namespace
@@ -1182,59 +1060,54 @@ Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t strea
                  0,
                  A.num_blocks};
     const BsrOpts o = opts ? *opts : BsrOpts{};
+    if (o.row_group != 0 && o.row_group != 1 && o.row_group != 4 && o.row_group != 8) {
+        return fail(kInvalid, "row_group must be 0, 1, 4 or 8");
+    }
     args.xcd_order = o.xcd_order == 2 ? 0 : 1;
     hipError_t e;
-    const int nwords = (A.block_cols + 31) / 32;
-    const bool use_groups = o.row_group != 0 && !o.per_wave && nwords <= kMaxUnionWords;
-    if (!use_groups) {
-        // Defaults of the wave kernel, from a sweep of 92 MI355X runs (uniform,
-        // banded, block-diagonal and power-law, M = 4096 .. 16384, N = 64 ..
-        // 512).  Four 16-column tiles per wave halve the A-block re-reads of
-        // two tiles and win once the grid still has >= 1024 waves at four
-        // tiles, unless block-rows are short (< 12 blocks) and the grid is
-        // under 2048 waves: then the extra waves of two tiles hide more latency
-        // (e.g. uniform 8192^2 density 0.01 N=128: 67 -> 48 us; banded 8192^2
-        // half-bandwidth 64 N=128 stays at two tiles, 4.0 vs 4.1 us).  Four
-        // pairs in flight pay on long block-rows: >= 30 blocks at two tiles,
-        // >= 96 at four (uniform 4096^2 density 0.01 N=128: 26.4 -> 20.3 us).
-        // The pointer-arithmetic form keeps two tiles and two pairs: it has no
-        // buffer-to-LDS staging, and four tiles measured slower there.
-        const bool rec = o.addressing != 1 && records_fit(args);
-        const double bpr = A.block_rows > 0 ? static_cast<double>(A.num_blocks) / A.block_rows : 0.0;
-        const long waves4 = static_cast<long>(A.block_rows) * ((N + 63) / 64);
-        const int j_auto =
-            N <= 16 ? 1
-                    : ((rec && waves4 >= 1024 && (bpr >= 12.0 || waves4 >= 2048)) ? 4 : 2);
-        const int j = (o.tiles == 1 || o.tiles == 2 || o.tiles == 4) ? o.tiles : j_auto;
-        const int d_auto = (rec && bpr >= (j == 4 ? 96.0 : 30.0)) ? 4 : 2;
-        const int d = (o.depth == 1 || o.depth == 2 || o.depth == 4) ? o.depth : d_auto;
-        if (o.split == 4) {
-            e = dispatch_splitk(j, d == 1 ? 1 : 2, args, stream);
-            return from_hip(e, "spmm_wmma launch");
+    const bool rec = o.addressing != 1 && records_fit(args);
+    const double bpr = A.block_rows > 0 ? static_cast<double>(A.num_blocks) / A.block_rows : 0.0;
+    // Shared-panel kernel (R = 4, 64 columns, 2 stages): automatic on wide B
+    // with long block-rows of structured inputs, the cells where it measured
+    // faster than the wave kernel (N >= 256, 24 - 64 blocks per block-row:
+    // 1.03 - 1.31x over 36 block-diagonal and banded inputs); explicit
+    // row_group 4 / 8 forces it.
+    const bool panel_auto = rec && N >= 256 && A.block_cols <= kPanelMaxWords * 32 &&
+                            bpr >= 24.0 && bpr <= 64.0;
+    const bool panel = !o.per_wave && rec &&
+                       (o.row_group == 4 || o.row_group == 8 || (o.row_group == 0 && panel_auto));
+    if (panel) {
+        const int R = o.row_group == 8 ? 8 : 4;
+        const int j = o.tiles == 8 ? 8 : 4;
+        const int d = o.depth == 4 ? 4 : 2;
+        if (R == 4) {
+            e = j == 4 ? dispatch_panel<4, 4>(d, args, stream) : dispatch_panel<4, 8>(d, args, stream);
+        } else {
+            e = j == 4 ? dispatch_panel<8, 4>(d, args, stream) : dispatch_panel<8, 8>(d, args, stream);
         }
-        if (o.rows == 2 || o.rows == 4) {
-            const int dm = d == 1 ? 1 : 2;
-            e = o.rows == 2 ? dispatch_multirow<2>(j, dm, args, stream)
-                            : dispatch_multirow<4>(j, dm, args, stream);
-            return from_hip(e, "spmm_wmma launch");
-        }
-        const bool ptr = o.addressing == 1;
-        e = j == 1 ? dispatch_wave<1>(d, ptr, args, stream)
-                   : (j == 2 ? dispatch_wave<2>(d, ptr, args, stream)
-                             : dispatch_wave<4>(d, ptr, args, stream));
         return from_hip(e, "spmm_wmma launch");
     }
-    int j = o.tiles;
-    if (j != 1 && j != 2 && j != 4 && j != 8) j = N <= 16 ? 1 : (N <= 32 ? 2 : 4);
-    if (o.row_group == 8) {
-        e = dispatch_rowgroup<8>(j, args, stream);
-    } else if (o.row_group == 2) {
-        e = dispatch_rowgroup<2>(j, args, stream);
-    } else if (o.row_group == 1) {
-        e = dispatch_rowgroup<1>(j, args, stream);
-    } else {
-        e = dispatch_rowgroup<4>(j, args, stream);
-    }
+    // Defaults of the wave kernel, from a sweep of 92 MI355X runs (uniform,
+    // banded, block-diagonal and power-law, M = 4096 .. 16384, N = 64 .. 512).
+    // Four 16-column tiles per wave halve the A-block re-reads of two tiles
+    // and win once the grid still has >= 1024 waves at four tiles, unless
+    // block-rows are short (< 12 blocks) and the grid is under 2048 waves:
+    // then the extra waves of two tiles hide more latency (e.g. uniform
+    // 8192^2 density 0.01 N=128: 67 -> 48 us).  Four pairs in flight pay on
+    // long block-rows: >= 30 blocks at two tiles, >= 96 at four (uniform
+    // 4096^2 density 0.01 N=128: 26.4 -> 20.3 us).  The pointer-arithmetic
+    // form keeps two tiles and two pairs: it has no buffer-to-LDS staging,
+    // and four tiles measured slower there.
+    const long waves4 = static_cast<long>(A.block_rows) * ((N + 63) / 64);
+    const int j_auto =
+        N <= 16 ? 1 : ((rec && waves4 >= 1024 && (bpr >= 12.0 || waves4 >= 2048)) ? 4 : 2);
+    const int j = (o.tiles == 1 || o.tiles == 2 || o.tiles == 4) ? o.tiles : j_auto;
+    const int d_auto = (rec && bpr >= (j == 4 ? 96.0 : 30.0)) ? 4 : 2;
+    const int d = (o.depth == 1 || o.depth == 2 || o.depth == 4) ? o.depth : d_auto;
+    const bool ptr = o.addressing == 1;
+    e = j == 1 ? dispatch_wave<1>(d, ptr, args, stream)
+               : (j == 2 ? dispatch_wave<2>(d, ptr, args, stream)
+                         : dispatch_wave<4>(d, ptr, args, stream));
     return from_hip(e, "spmm_wmma launch");
 }
 

@@ -645,8 +645,6 @@ int spmm_c_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B16, float* d_C,
         o.per_wave  = opts->per_wave;
         o.depth     = opts->depth;
         o.xcd_order = opts->xcd_order;
-        o.rows      = opts->rows;
-        o.split     = opts->split;
         o.addressing = opts->addressing;
     }
     return from_engine(spmm::engine::launch_bsr(to_cpp(*d_bsr),

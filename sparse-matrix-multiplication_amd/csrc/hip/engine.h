@@ -78,17 +78,18 @@ Error launch_csr(CsrRole role, const CSR& d_A, const float* d_B, float* d_C, int
 Error launch_float_to_half(const float* d_src, half* d_dst, long n, hipStream_t stream);
 
 // Tuning of the BSR matrix-core kernels.  All zero selects the default: the
-// wave kernel (one independent wave per block-row) with tiles and depth
-// chosen from N.
+// shared-panel kernel on wide B with long structured block-rows (N >= 256, 24
+// - 64 blocks per block-row), else the wave kernel, with shapes from N.
 struct BsrOpts {
-    int row_group = 0;  // 0: wave kernel; 1, 2, 4, 8: block-rows per workgroup sharing B tiles
-    int tiles     = 0;  // 16-column MFMA tiles per wave: 1, 2, 4 (8 with row groups)
-    int per_wave  = 0;  // 1: wave kernel whatever row_group says
-    int depth     = 0;  // wave kernel: block pairs in flight per wave, 1, 2 or 4
-    int xcd_order = 0;  // wave kernel: 0, 1 XCD-grouped workgroup order; 2 dispatch order
-    int rows      = 0;  // wave kernel: block-rows per wave sharing staged B tiles, 1, 2 or 4
-    int split     = 0;  // wave kernel: 4 = the four waves of a workgroup split one block-row
-    int addressing = 0; // wave kernel: 0 buffer records where they fit, 1 pointer arithmetic
+    int row_group  = 0;  // 0: automatic; 1: wave kernel; 4, 8: panel kernel with that many
+                         // block-rows per workgroup sharing staged B tiles
+    int tiles      = 0;  // wave kernel: 16-column tiles per wave, 1, 2, 4;
+                         // panel kernel: 16-column tiles per workgroup, 4 or 8
+    int per_wave   = 0;  // 1: wave kernel whatever row_group says
+    int depth      = 0;  // wave kernel: block pairs in flight per wave, 1, 2 or 4;
+                         // panel kernel: LDS stages in flight, 2 or 4
+    int xcd_order  = 0;  // 0, 1 XCD-grouped workgroup order; 2 dispatch order
+    int addressing = 0;  // 0 buffer records where they fit, 1 pointer arithmetic (wave kernel)
 };
 
 Error launch_bsr(const BSR& d_A, const half* d_B, float* d_C, int N, hipStream_t stream,

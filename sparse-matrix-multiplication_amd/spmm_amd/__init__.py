@@ -74,8 +74,8 @@ class EngineOptsT(ctypes.Structure):
 
 class BsrOptsT(ctypes.Structure):
     _fields_ = [("row_group", ctypes.c_int), ("tiles", ctypes.c_int), ("per_wave", ctypes.c_int),
-                ("depth", ctypes.c_int), ("xcd_order", ctypes.c_int), ("rows", ctypes.c_int),
-                ("split", ctypes.c_int), ("addressing", ctypes.c_int)]
+                ("depth", ctypes.c_int), ("xcd_order", ctypes.c_int),
+                ("addressing", ctypes.c_int)]
 
 
 _P = ctypes.POINTER

@@ -91,20 +91,26 @@ def test_wmma_cases(S, O, torch, name):
     check_csr(C, C64, absC, tol=1e-5)
 
 
-@pytest.mark.parametrize("row_group,tiles,per_wave", [(1, 1, 0), (1, 2, 0), (1, 4, 0), (1, 8, 0),
-                                                       (2, 2, 0), (2, 4, 0), (2, 8, 0),
-                                                       (4, 1, 0), (4, 2, 0), (4, 4, 0), (4, 8, 0),
-                                                       (8, 1, 0), (8, 4, 0), (8, 8, 0),
-                                                       (0, 1, 1), (0, 2, 1), (0, 4, 1)])
-@pytest.mark.parametrize("depth", [1, 2, 4])
-@pytest.mark.parametrize("addressing", [0, 1])
+def _variants():
+    """(row_group, tiles, per_wave, depth, addressing) combinations that apply:
+    the wave kernel (row_group 1, or per_wave) with 1/2/4 tiles per wave, 1/2/4
+    pairs in flight and both addressings; the shared-panel kernel with 4 or 8
+    block-rows per workgroup, 4 or 8 tiles per workgroup, 2/3/4 stages."""
+    out = []
+    for tiles in (1, 2, 4):
+        for depth in (1, 2, 4):
+            for addressing in (0, 1):
+                out.append((1, tiles, 0, depth, addressing))
+                out.append((0, tiles, 1, depth, addressing))
+    for rg in (4, 8):
+        for tiles in (4, 8):
+            for depth in (2, 4, 8):
+                out.append((rg, tiles, 0, depth, 0))
+    return out
+
+
+@pytest.mark.parametrize("row_group,tiles,per_wave,depth,addressing", _variants())
 def test_wmma_variants(S, O, torch, row_group, tiles, per_wave, depth, addressing):
-    # addressing 0: B rows and A blocks as buffer records (tiles >= 2, N % 8 == 0),
-    # 1: the pointer-arithmetic wave kernel
-    if depth != 2 and (row_group != 0 or per_wave == 0):
-        pytest.skip("depth applies to the wave kernel only")
-    if addressing == 1 and per_wave == 0:
-        pytest.skip("addressing applies to the wave kernel only")
     cases = _cases(S)
     for name in ("single_block", "odd_pair_count", "ragged_dims", "n_not_16", "n_1",
                  "empty_block_rows", "empty", "wide_n", "block_diag_small"):
@@ -115,8 +121,7 @@ def test_wmma_variants(S, O, torch, row_group, tiles, per_wave, depth, addressin
         dA = S.DeviceBSR(hb)
         dB = torch.from_numpy(B16.view(np.int16)).cuda()
         dC = torch.full((hb.num_rows, B16.shape[1]), float("nan"), device="cuda")
-        S.spmm_wmma_opts(dA, dB, S.BsrOptsT(row_group, tiles, per_wave, depth, 0, 0, 0,
-                                            addressing), dC)
+        S.spmm_wmma_opts(dA, dB, S.BsrOptsT(row_group, tiles, per_wave, depth, 0, addressing), dC)
         torch.cuda.synchronize()
         C = dC.cpu().numpy()
         check_bsr(C, C32, absC)
@@ -124,17 +129,19 @@ def test_wmma_variants(S, O, torch, row_group, tiles, per_wave, depth, addressin
 
 
 def test_wmma_long_block_rows(S, O, torch):
-    # block-rows with more than 64 blocks (the per-wave register chunk) and a
-    # union wider than one bitmap word
+    # block-rows with more than 64 blocks (the wave kernel's register chunk);
+    # for the panel kernel a union wider than one pass of 256 slots
     A = S.generate_uniform_random_csr(64, 2048, 0.05, 31)
     A.values = S.round_to_fp16(A.values)
     B = S.round_to_fp16(np.random.default_rng(3).uniform(-1, 1, (2048, 64)).astype(np.float32))
     hb, B16, C32, C64, absC = _refs(S, O, A, B)
     assert np.diff(hb.row_ptr).max() > 64
-    for rg, tiles in ((4, 4), (8, 4), (0, 1), (0, 2), (0, 4)):
-        say(f"wmma long block-rows row_group={rg} tiles={tiles} blocks={hb.num_blocks}")
+    for rg, tiles, depth in ((4, 4, 2), (4, 8, 8), (8, 4, 4), (8, 8, 4), (1, 1, 0), (1, 2, 0),
+                             (1, 4, 4)):
+        say(f"wmma long block-rows row_group={rg} tiles={tiles} depth={depth} "
+            f"blocks={hb.num_blocks}")
         C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
-                             S.BsrOptsT(rg, tiles, 0)).cpu().numpy()
+                             S.BsrOptsT(rg, tiles, 0, depth)).cpu().numpy()
         check_bsr(C, C32, absC)
         check_csr(C, C64, absC, tol=1e-5)
 
@@ -158,106 +165,114 @@ def test_wmma_chunk_boundaries(S, O, torch):
             for addressing in (0, 1):
                 say(f"wmma chunk boundaries tiles={tiles} depth={depth} addressing={addressing}")
                 C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
-                                     S.BsrOptsT(0, tiles, 1, depth, 0, 0, 0,
+                                     S.BsrOptsT(1, tiles, 0, depth, 0,
                                                 addressing)).cpu().numpy()
                 check_bsr(C, C32, absC)
                 check_csr(C, C64, absC, tol=1e-5)
 
 
-@pytest.mark.parametrize("rows", [2, 4])
-@pytest.mark.parametrize("tiles,depth", [(1, 1), (1, 2), (2, 1), (2, 2), (4, 1), (4, 2)])
-def test_wmma_multirow(S, O, torch, rows, tiles, depth):
-    # R block-rows per wave walking the union of their block-columns: banded
-    # and block-diagonal (shared columns), random (mostly disjoint), empty and
-    # ragged block-rows, block-row counts not divisible by 4R
-    cases = _cases(S)
-    for name in ("single_block", "odd_pair_count", "ragged_dims", "n_not_16", "n_1",
-                 "empty_block_rows", "empty", "wide_n", "block_diag_small"):
-        A, B = cases[name]
-        hb, B16, C32, C64, absC = _refs(S, O, A, B)
-        say(f"wmma multirow rows={rows} tiles={tiles} depth={depth} case={name}")
-        dC = torch.full((hb.num_rows, B16.shape[1]), float("nan"), device="cuda")
-        S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
-                         S.BsrOptsT(0, tiles, 0, depth, 0, rows), dC)
-        torch.cuda.synchronize()
-        C = dC.cpu().numpy()
+def _dev_bsr(S, torch, M, K, row_ptr, col_idx, values16):
+    """A device BSR from raw arrays (block-columns in any order, repeats allowed)."""
+    hb = S.HostBSR(M, K, (M + 15) // 16, (K + 15) // 16, 0, np.asarray(row_ptr, np.int32),
+                   np.asarray(col_idx, np.int32), np.asarray(values16, np.uint16))
+    return hb, S.DeviceBSR(hb)
+
+
+@pytest.mark.parametrize("order", ["descending", "repeated", "out_of_range"])
+def test_panel_identity_union(S, O, torch, order):
+    # Block-column lists that are not strictly ascending (or name block-columns
+    # outside the matrix) take the panel kernel's identity union; the result
+    # is the plain sum over the stored blocks either way.
+    rng = np.random.default_rng(11)
+    M, K, N = 80, 96, 64
+    br, bc = (M + 15) // 16, (K + 15) // 16
+    lists = [list(rng.choice(bc, int(rng.integers(1, bc + 1)), replace=False)) for _ in range(br)]
+    if order == "descending":
+        lists = [sorted(l, reverse=True) for l in lists]
+    elif order == "repeated":
+        lists = [sorted(l + l[:2]) for l in lists]
+    else:
+        lists = [sorted(l) + [bc + 3] for l in lists]
+    row_ptr = np.concatenate([[0], np.cumsum([len(l) for l in lists])])
+    col_idx = np.concatenate(lists)
+    vals = O.f32_to_f16(rng.uniform(-1, 1, len(col_idx) * 256).astype(np.float32))
+    B = S.round_to_fp16(rng.uniform(-1, 1, (K, N)).astype(np.float32))
+    B16 = O.f32_to_f16(B)
+    # dense reference: stored blocks summed (columns beyond K contribute nothing)
+    Ad = np.zeros((br * 16, (bc + 4) * 16))
+    v = vals.view(np.float16).astype(np.float64).reshape(-1, 16, 16)
+    for r in range(br):
+        for p in range(row_ptr[r], row_ptr[r + 1]):
+            Ad[r * 16:(r + 1) * 16, col_idx[p] * 16:(col_idx[p] + 1) * 16] += v[p]
+    Bd = np.zeros(((bc + 4) * 16, N))
+    Bd[:K] = B
+    want = (Ad @ Bd)[:M]
+    absC = (np.abs(Ad) @ np.abs(Bd))[:M]
+    hb, dA = _dev_bsr(S, torch, M, K, row_ptr, col_idx, vals)
+    for rg, tiles in ((4, 4), (8, 8)):
+        say(f"panel identity union order={order} row_group={rg} tiles={tiles}")
+        C = S.spmm_wmma_opts(dA, torch.from_numpy(B16.view(np.int16)).cuda(),
+                             S.BsrOptsT(rg, tiles, 0, 3)).cpu().numpy()
+        check_csr(C, want, absC, tol=1e-5)
+
+
+def test_panel_wide_matrix_identity(S, O, torch):
+    # K beyond the union bitmap (8192 block-columns): identity union
+    A = S.generate_uniform_random_csr(48, 140000, 0.0004, 12)
+    A.values = S.round_to_fp16(A.values)
+    B = S.round_to_fp16(np.random.default_rng(13).uniform(-1, 1, (140000, 64)).astype(np.float32))
+    hb, B16, C32, C64, absC = _refs(S, O, A, B)
+    assert hb.block_cols > 8192
+    for rg in (4, 8):
+        say(f"panel wide K={A.num_cols} row_group={rg}")
+        C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
+                             S.BsrOptsT(rg, 4, 0, 2)).cpu().numpy()
         check_bsr(C, C32, absC)
         check_csr(C, C64, absC, tol=1e-5)
 
 
-@pytest.mark.parametrize("rows", [2, 4])
-def test_wmma_multirow_long_and_chunked(S, O, torch, rows):
-    # more than 64 blocks over the R block-rows (block-row by block-row in
-    # chunks of 64) next to groups that merge
-    rowsl, cols = [], []
-    for br, nb in enumerate((63, 64, 65, 128, 129, 1, 0, 2, 3, 5, 30, 31)):
-        for b in range(nb):
-            rowsl.append(br * 16 + (b % 16))
-            cols.append(((b * 7 + br) % 130) * 16 + (br % 16))
-    A = S.csr_from_coo_host(12 * 16, 130 * 16, np.array(rowsl), np.array(cols),
-                            np.random.default_rng(5).uniform(-1, 1, len(rowsl)).astype(np.float32))
-    A.values = S.round_to_fp16(A.values)
-    B = S.round_to_fp16(np.random.default_rng(6).uniform(-1, 1, (130 * 16, 48)).astype(np.float32))
-    hb, B16, C32, C64, absC = _refs(S, O, A, B)
-    for tiles in (1, 2, 4):
-        for depth in (1, 2):
-            say(f"wmma multirow chunks rows={rows} tiles={tiles} depth={depth}")
-            C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
-                                 S.BsrOptsT(0, tiles, 0, depth, 0, rows)).cpu().numpy()
-            check_bsr(C, C32, absC)
-            check_csr(C, C64, absC, tol=1e-5)
-
-
-@pytest.mark.parametrize("rows", [2, 4])
+@pytest.mark.parametrize("rg,tiles,depth", [(4, 4, 2), (4, 4, 8), (4, 8, 4), (4, 8, 8),
+                                            (8, 4, 8), (8, 8, 2), (8, 8, 4)])
 @pytest.mark.parametrize("cfg", ["c3", "c4"])
-def test_wmma_multirow_configs(S, O, torch, rows, cfg):
+def test_panel_configs(S, O, torch, rg, tiles, depth, cfg):
     A, B = make_config(S, cfg)
     hb, B16, C32, C64, absC = _refs(S, O, A, B)
-    say(f"wmma multirow config={cfg} rows={rows}")
+    say(f"panel config={cfg} row_group={rg} tiles={tiles} depth={depth}")
     C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
-                         S.BsrOptsT(0, 0, 0, 0, 0, rows)).cpu().numpy()
+                         S.BsrOptsT(rg, tiles, 0, depth)).cpu().numpy()
     check_bsr(C, C32, absC)
     check_csr(C, C64, absC, tol=1e-5)
 
 
-@pytest.mark.parametrize("tiles,depth", [(1, 1), (1, 2), (2, 1), (2, 2), (4, 1), (4, 2)])
-def test_wmma_split(S, O, torch, tiles, depth):
-    # the four waves of a workgroup share one block-row (pairs w, w+4, ...)
-    # and add their partial tiles through LDS
-    cases = _cases(S)
-    for name in ("single_block", "odd_pair_count", "ragged_dims", "n_not_16", "n_1",
-                 "empty_block_rows", "empty", "wide_n", "block_diag_small"):
-        A, B = cases[name]
+def test_panel_structured_shapes(S, O, torch):
+    # banded and block-diagonal matrices whose blocks straddle block-rows,
+    # ragged M / K, a partial last column tile (N = 200), and a union that
+    # takes several 256-slot passes (dense block-rows, K = 6000)
+    rng = np.random.default_rng(21)
+    mats = [("banded_hb3", S.generate_banded_csr(200, 200, 3, 1), 200),
+            ("banded_hb100", S.generate_banded_csr(1000, 1030, 100, 2), 128),
+            ("block_diag_40", S.generate_block_diagonal_csr(500, 500, 40, 3, 1.0), 64),
+            ("block_diag_256_n200", S.generate_block_diagonal_csr(1024, 1024, 256, 4, 1.0), 200),
+            ("dense_rows_k6000", S.generate_uniform_random_csr(70, 6000, 0.2, 5), 64)]
+    for name, A, N in mats:
+        A.values = S.round_to_fp16(A.values)
+        B = S.round_to_fp16(rng.uniform(-1, 1, (A.num_cols, N)).astype(np.float32))
         hb, B16, C32, C64, absC = _refs(S, O, A, B)
-        say(f"wmma split tiles={tiles} depth={depth} case={name}")
-        dC = torch.full((hb.num_rows, B16.shape[1]), float("nan"), device="cuda")
-        S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
-                         S.BsrOptsT(0, tiles, 0, depth, 0, 0, 4), dC)
-        torch.cuda.synchronize()
-        C = dC.cpu().numpy()
-        check_bsr(C, C32, absC)
-        check_csr(C, C64, absC, tol=1e-5)
-
-
-def test_wmma_split_chunks_and_configs(S, O, torch):
-    rowsl, cols = [], []
-    for br, nb in enumerate((63, 64, 65, 128, 129, 1, 0, 2, 3, 5, 7, 9)):
-        for b in range(nb):
-            rowsl.append(br * 16 + (b % 16))
-            cols.append(((b * 7 + br) % 130) * 16 + (br % 16))
-    A = S.csr_from_coo_host(12 * 16, 130 * 16, np.array(rowsl), np.array(cols),
-                            np.random.default_rng(5).uniform(-1, 1, len(rowsl)).astype(np.float32))
-    A.values = S.round_to_fp16(A.values)
-    B = S.round_to_fp16(np.random.default_rng(6).uniform(-1, 1, (130 * 16, 48)).astype(np.float32))
-    mats = [("chunks", A, B)] + [(c, *make_config(S, c)) for c in ("c3", "c4")]
-    for name, A, B in mats:
-        hb, B16, C32, C64, absC = _refs(S, O, A, B)
-        for tiles, depth in ((1, 2), (2, 1), (2, 2), (4, 2)):
-            say(f"wmma split {name} tiles={tiles} depth={depth}")
+        for rg, tiles, depth in ((4, 4, 8), (4, 8, 2), (8, 8, 4), (0, 0, 0)):
+            say(f"panel {name} N={N} row_group={rg} tiles={tiles} depth={depth}")
             C = S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(),
-                                 S.BsrOptsT(0, tiles, 0, depth, 0, 0, 4)).cpu().numpy()
+                                 S.BsrOptsT(rg, tiles, 0, depth)).cpu().numpy()
             check_bsr(C, C32, absC)
             check_csr(C, C64, absC, tol=1e-5)
+
+
+def test_wmma_bad_row_group(S, torch):
+    A = S.generate_banded_csr(64, 64, 3, 1)
+    dA = S.DeviceBSR(S.bsr_from_csr_host(A))
+    B16 = torch.zeros((64, 64), dtype=torch.float16, device="cuda")
+    with pytest.raises(S.SpmmError) as e:
+        S.spmm_wmma_opts(dA, B16, S.BsrOptsT(2, 0, 0, 0))
+    assert e.value.code == S.SPMM_INVALID
 
 
 @pytest.mark.parametrize("xcd_order", [1, 2])

@@ -112,7 +112,14 @@ def test_mfma_random(S, O, torch, chunk):
     rng = np.random.default_rng(2000 + chunk)
     for case in range(25):
         M, K, N = _shape(rng)
-        A = _random_csr(S, rng, M, K)
+        shape = int(rng.integers(0, 5))
+        if shape == 3:    # banded: neighbouring block-rows share block-columns
+            A = S.generate_banded_csr(M, K, int(rng.integers(0, 80)), int(rng.integers(1, 10000)))
+        elif shape == 4:  # block-diagonal, block sizes not multiples of 16 included
+            A = S.generate_block_diagonal_csr(M, K, int(rng.integers(1, 100)),
+                                              int(rng.integers(1, 10000)), 1.0)
+        else:
+            A = _random_csr(S, rng, M, K)
         A.values = S.round_to_fp16(A.values)
         B = S.round_to_fp16(rng.uniform(-1, 1, (K, N)).astype(np.float32))
         hb = S.bsr_from_csr_host(A)
@@ -120,11 +127,16 @@ def test_mfma_random(S, O, torch, chunk):
         C32 = O.bsr_spmm_f32(M, K, hb.row_ptr, hb.col_idx, hb.values, B16, threads=8)
         C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B16.view(np.float16)
                                    .astype(np.float32), threads=8)
-        opts = S.BsrOptsT(0, int(rng.choice([0, 1, 2, 4])), 1, int(rng.choice([0, 1, 2, 4])),
-                          int(rng.choice([0, 1, 2])), 0, 0, int(rng.choice([0, 1])))
+        kernel = int(rng.choice([0, 1, 4, 8]))  # automatic, wave, panel R = 4 / 8
+        if kernel == 1:
+            opts = S.BsrOptsT(1, int(rng.choice([0, 1, 2, 4])), 1, int(rng.choice([0, 1, 2, 4])),
+                              int(rng.choice([0, 1, 2])), int(rng.choice([0, 1])))
+        else:
+            opts = S.BsrOptsT(kernel, int(rng.choice([0, 4, 8])), 0, int(rng.choice([0, 2, 3, 4])),
+                              int(rng.choice([0, 1, 2])), 0)
         say(f"fuzz mfma chunk={chunk} case={case} M={M} K={K} N={N} blocks={hb.num_blocks} "
-            f"opts=(tiles {opts.tiles}, depth {opts.depth}, order {opts.xcd_order}, "
-            f"addressing {opts.addressing})")
+            f"opts=(row_group {opts.row_group}, tiles {opts.tiles}, depth {opts.depth}, "
+            f"order {opts.xcd_order}, addressing {opts.addressing})")
         dC = torch.full((M, N), float("nan"), device="cuda")
         S.spmm_wmma_opts(S.DeviceBSR(hb), torch.from_numpy(B16.view(np.int16)).cuda(), opts, dC)
         torch.cuda.synchronize()

@@ -222,6 +222,15 @@ int spmm_c_nnz_split_rows(const spmm_csr_t* h, int parts, int* h_rows_out);
 int spmm_c_split_partition_parts(int nnz);
 int spmm_c_tiled_v3_split(const spmm_csr_t* d_A, const int* d_split_rows, int parts,
                           const float* d_B, float* d_C, int N, float* d_carry, void* stream);
+/* spmm_c_tiled_v3_split without the caller's workspace: the carries live in a
+ * file-scope device array of 2^19 floats (2 MiB) that each GPU holds from the
+ * first call on it until the process ends.  No counterpart in the reference:
+ * it is for callers that cannot allocate (HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc); it calls no allocating routine.  parts x
+ * N above 2^19 returns SPMM_UNSUPPORTED.  All calls on one GPU share its array:
+ * calls that overlap on one GPU race. */
+int spmm_c_tiled_v3_split_noalloc(const spmm_csr_t* d_A, const int* d_split_rows, int parts,
+                                  const float* d_B, float* d_C, int N, void* stream);
 /* The CSR form spmm_hybrid_run's CSR branch picks for host CSR h and a B of N
  * columns (no counterpart in the reference): *form_out = 0 the row-block
  * engine, 1 sub-wave row groups, 2 the merge-path partition; *opts_out the

@@ -596,6 +596,13 @@ int spmm_c_tiled_v3_split(const spmm_csr_t* d_A, const int* d_split_rows, int pa
                                                       as_stream(stream), plan));
 }
 
+int spmm_c_tiled_v3_split_noalloc(const spmm_csr_t* d_A, const int* d_split_rows, int parts,
+                                  const float* d_B, float* d_C, int N, void* stream) {
+    if (d_A == nullptr || d_split_rows == nullptr) return set_error(SPMM_INVALID, "null argument");
+    return from_engine(spmm::engine::launch_csr_split_noalloc(to_cpp(*d_A), d_split_rows, parts,
+                                                              d_B, d_C, N, as_stream(stream)));
+}
+
 int spmm_c_split_partition_parts(int nnz) { return spmm::engine::split_partition_parts(nnz); }
 
 int spmm_c_csr_auto_form(const spmm_csr_t* h, int N, int* form_out, spmm_engine_opts_t* opts_out,

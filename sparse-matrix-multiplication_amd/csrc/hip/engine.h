@@ -128,6 +128,13 @@ struct SplitPlan {
 };
 Error launch_csr_split(const CSR& d_A, const float* d_B, float* d_C, int N, hipStream_t stream,
                        const SplitPlan& plan, const EngineOpts* opts = nullptr);
+// The same launch with the carry workspace taken from a file-scope device
+// array (noalloc.hip) instead of the caller: allocates nothing, shares one
+// workspace per GPU (overlapping calls on a GPU race), and refuses parts x N
+// beyond noalloc_scratch_floats() floats.
+Error launch_csr_split_noalloc(const CSR& d_A, const int* d_split_rows, int parts,
+                               const float* d_B, float* d_C, int N, hipStream_t stream);
+long noalloc_scratch_floats();
 // Parts of the merge-path partition for nnz nonzeros, and whether it beats
 // the row partition for a matrix whose longest row has max_row_nnz entries.
 int split_partition_parts(int nnz);

@@ -127,6 +127,7 @@ _SIGNATURES = {
     "spmm_c_nnz_split_rows": (_int, [_P(CsrT), _int, _vp]),
     "spmm_c_split_partition_parts": (_int, [_int]),
     "spmm_c_tiled_v3_split": (_int, [_P(CsrT), _vp, _int, _vp, _vp, _int, _vp, _vp]),
+    "spmm_c_tiled_v3_split_noalloc": (_int, [_P(CsrT), _vp, _int, _vp, _vp, _int, _vp]),
     "spmm_c_launch_repeat_split": (_int, [_P(CsrT), _vp, _int, _vp, _vp, _int, _vp, _int, _vp]),
     "spmm_c_default_partition_parts": (_int, [_int, _int]),
     "spmm_c_csr_auto_form": (_int, [_P(CsrT), _int, _P(ctypes.c_int),
@@ -718,6 +719,19 @@ def _check_split(split_rows, B, N: int, carry) -> int:
             raise SpmmError(SPMM_INVALID, f"carry: {carry.numel()} floats, needs parts * N = "
                                           f"{parts * N}")
     return parts
+
+
+def spmm_tiled_v3_split_noalloc(A: DeviceCSR, split_rows, B, C=None, stream=None):
+    """Merge-path partition with the carries in the library's per-GPU device
+    array (allocates nothing; parts x N <= 2**19; overlapping calls on one GPU
+    race)."""
+    N, C = _csr_operands(A, B, C)
+    parts = _check_split(split_rows, B, N, None)
+    s = A.struct()
+    _check(lib().spmm_c_tiled_v3_split_noalloc(ctypes.byref(s), split_rows.data_ptr(), parts,
+                                               B.data_ptr(), C.data_ptr(), N,
+                                               _stream_handle(stream)))
+    return C
 
 
 def launch_repeat_split(A: DeviceCSR, split_rows, B, C, carry, reps: int, stream=None) -> None:

@@ -105,7 +105,8 @@ typedef struct spmm_engine_opts_t {
     int max_row_hint;   /* longest row's entries if known (0 = unknown).
                            row_groups != 0: lets the kernel drop its long-row
                            pass when no row needs it (a hint below the true
-                           longest row gives wrong results for the longer rows).
+                           longest row is still correct: each group then sums
+                           its long row itself, which only costs time).
                            row_groups == 0: the row-block engine (also for the
                            narrow B that takes row groups by default); rows
                            within 2 x average + 32 entries give it a grid of

@@ -55,8 +55,9 @@ struct EngineOpts {
     int entry_lanes    = 0;  // row groups: entry lanes per row, a power of two up to 64
     // The longest row's entries when the caller knows it (0 = unknown).
     // row_groups != 0: with no row longer than the long-row cut, the kernel
-    // is built without its workgroup-wide pass; a hint below the true longest
-    // row gives wrong results for the longer rows.  row_groups == 0: the
+    // is built without its workgroup-wide pass; with a hint below the true
+    // longest row each group sums its long row itself (correct, slower).
+    // row_groups == 0: the
     // row-block engine (a hint also keeps narrow B off the default row
     // groups); rows within 2 x average + 32 entries give its implicit
     // partition a grid of whole rounds of 4-wave workgroups instead of ~160

@@ -50,6 +50,15 @@ def _matrices(S):
     return out
 
 
+def _equals_oracle(O, A, dev):
+    """The device build is bitwise the oracle's restatement of bsr_from_csr_host
+    (bsr.cu:30-109): block row pointers, ascending block-columns, RNE fp16."""
+    brp, bci, bv = O.bsr_build(A.num_rows, A.num_cols, A.row_ptr, A.col_idx, A.values)
+    assert np.array_equal(dev.row_ptr, brp)
+    assert np.array_equal(dev.col_idx, bci)
+    assert np.array_equal(dev.values, bv)
+
+
 def _build_both(S, A):
     host = S.bsr_from_csr_host(A)
     built = S.bsr_from_csr_device(S.DeviceCSR(A))
@@ -60,10 +69,11 @@ def _build_both(S, A):
 @pytest.mark.parametrize("name", ["uniform_small", "ragged_dims", "banded", "block_diag",
                                   "power_law", "empty_nnz", "one_by_one", "k_is_1", "wide_k",
                                   "duplicates", "rounding"])
-def test_device_build_equals_host(S, torch, name):
+def test_device_build_equals_host(S, O, torch, name):
     A = _matrices(S)[name]
     say(f"bsr build case={name} M={A.num_rows} K={A.num_cols} nnz={A.nnz}")
     host, dev, built = _build_both(S, A)
+    _equals_oracle(O, A, dev)
     assert (dev.num_rows, dev.num_cols, dev.block_rows, dev.block_cols, dev.nnz) == \
         (host.num_rows, host.num_cols, host.block_rows, host.block_cols, host.nnz)
     assert np.array_equal(dev.row_ptr, host.row_ptr)
@@ -76,10 +86,11 @@ def test_device_build_equals_host(S, torch, name):
 
 
 @pytest.mark.parametrize("cfg", ["c1", "c3", "c4", "c5"])
-def test_device_build_configs_and_product(S, torch, cfg):
+def test_device_build_configs_and_product(S, O, torch, cfg):
     A, B = make_config(S, cfg)
     say(f"bsr build config={cfg} nnz={A.nnz}")
     host, dev, built = _build_both(S, A)
+    _equals_oracle(O, A, dev)
     assert np.array_equal(dev.row_ptr, host.row_ptr)
     assert np.array_equal(dev.col_idx, host.col_idx)
     assert np.array_equal(dev.values, host.values)

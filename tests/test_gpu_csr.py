@@ -312,6 +312,26 @@ def test_row_groups_max_row_hint(S, torch, edge_cases, form):
         check_csr(_run_opts(S, torch, A, B, opts), C64, absC)
 
 
+@pytest.mark.parametrize("form", [1, 2, 3])
+def test_row_groups_undersized_hint(S, O, torch, form):
+    # A hint below the true longest row drops the workgroup-wide long-row
+    # pass; each group then sums its long row itself: slower, same result.
+    # Rows of 2 entries with 3% long rows (up to K entries, a 4096-entry one).
+    rng = np.random.default_rng(91)
+    M, K, N = 3000, 4096, 32
+    lens = np.where(rng.random(M) < 0.03, rng.integers(200, K + 1, M), 2)
+    lens[17] = K
+    rows = np.repeat(np.arange(M), lens)
+    cols = np.concatenate([rng.choice(K, n, replace=False) for n in lens])
+    A = S.csr_from_coo_host(M, K, rows, cols, rng.uniform(-1, 1, rows.size).astype(np.float32))
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)
+    for hint in (1, 2, 64, K):
+        say(f"csr row groups undersized hint={hint} (true {K}) form={form}")
+        opts = S.EngineOptsT(0, 0, 0, 0, 0, 0, 0, form, 0, hint)
+        check_csr(_run_opts(S, torch, A, B, opts), C64, absC)
+
+
 @pytest.mark.parametrize("hint_kind", ["true", "average", "one"])
 def test_engine_whole_round_grid(S, O, torch, edge_cases, hint_kind):
     # the row-block engine with a longest-row hint: rows within 2 x average +

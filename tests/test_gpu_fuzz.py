@@ -163,8 +163,10 @@ def _long_row_csr(S, rng, M, K):
 @pytest.mark.parametrize("chunk", range(2))
 def test_row_groups_random(S, O, torch, chunk):
     # the sub-wave row groups under random shapes, skew, load forms, column
-    # slices, entry lanes, unroll and longest-row hints (exact or above the
-    # true longest row), plus the default launch (row groups for N <= 32)
+    # slices, entry lanes, unroll and longest-row hints (exact, above, and
+    # below the true longest row: an under-sized hint drops the workgroup-wide
+    # long-row pass, so each group sums its long row itself), plus the default
+    # launch (row groups for N <= 32)
     rng = np.random.default_rng(3000 + chunk)
     for case in range(40):
         M = int(rng.integers(1, 1500))
@@ -176,7 +178,7 @@ def test_row_groups_random(S, O, torch, chunk):
         opts = S.EngineOptsT(int(rng.choice([0, 1, 2, 4])), 0, int(rng.choice([0, 2, 4])), 0, 0,
                              int(rng.choice([0, 1, 2, 4, 8])), 0, int(rng.choice([1, 2, 3])),
                              int(rng.choice([0, 1, 2, 4, 8, 16, 64])),
-                             int(rng.choice([0, mx, mx + 5])))
+                             int(rng.choice([0, mx, mx + 5, max(1, mx // 3), 1])))
         say(f"fuzz row groups chunk={chunk} case={case} M={M} K={K} N={N} nnz={A.nnz} max={mx} "
             f"opts=({opts.vec},{opts.unroll},{opts.slices},{opts.row_groups},{opts.entry_lanes},"
             f"{opts.max_row_hint})")

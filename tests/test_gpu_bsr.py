@@ -266,6 +266,29 @@ def test_panel_structured_shapes(S, O, torch):
             check_csr(C, C64, absC, tol=1e-5)
 
 
+def test_wmma_c_alignment(S, O, torch):
+    # The record kernel writes C in 16-byte row chunks when C is 16-byte
+    # aligned and in single floats otherwise: both give the same bits.
+    A, B = _cases(S)["block_diag_small"]
+    hb, B16, C32, C64, absC = _refs(S, O, A, B)
+    dA = S.DeviceBSR(hb)
+    dB = torch.from_numpy(B16.view(np.int16)).cuda()
+    M, N = hb.num_rows, B16.shape[1]
+    for tiles in (1, 2, 4):
+        aligned = torch.full((M, N), float("nan"), device="cuda")
+        flat = torch.full((M * N + 1,), float("nan"), device="cuda")
+        shifted = flat[1:].view(M, N)  # 4 bytes past a 16-byte boundary
+        assert shifted.data_ptr() % 16 == 4
+        say(f"wmma C alignment tiles={tiles}")
+        S.spmm_wmma_opts(dA, dB, S.BsrOptsT(1, tiles, 0, 2), aligned)
+        S.spmm_wmma_opts(dA, dB, S.BsrOptsT(1, tiles, 0, 2), shifted)
+        torch.cuda.synchronize()
+        a, b = aligned.cpu().numpy(), shifted.cpu().numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert np.isnan(flat[0].item())  # nothing written before C
+        check_bsr(a, C32, absC)
+
+
 def test_wmma_bad_row_group(S, torch):
     A = S.generate_banded_csr(64, 64, 3, 1)
     dA = S.DeviceBSR(S.bsr_from_csr_host(A))

@@ -13,7 +13,11 @@ One step = one pass of the hot path over inputs already resident in HBM
 steps, then K steps back to back on torch's current stream between two events
 on that stream, synchronised on both sides.  `cold_ms_median` is the median of
 single launches each preceded by a 512 MiB write that evicts L2 (4 MiB per
-XCD) and the 256 MB MALL; warm is the contract figure.
+XCD) and the 256 MB MALL; warm is the contract figure.  `graph_ms_per_step`
+is the same launches captured 100 at a time in one HIP graph and replayed (a
+replay is first checked bit for bit against the eager result): what a caller
+that captures its SpMM calls gets, reported beside the eager figure, never as
+`value`.
 
 Roofline units (scripts/roofline.py:177-185, harness.cu:239,278-280):
   CSR bytes = 8*nnz + 4*(M+1) + 4*K*N + 4*M*N, FLOPs = 2*nnz*N
@@ -122,7 +126,7 @@ def build_pattern(S, torch, name: str):
     pattern, M, N, fp16, desc = CONFIGS[name]
     A, B = make_config(S, name)
     plan = S.hybrid_choose(A, N)
-    stream = torch.cuda.current_stream()
+    cur = torch.cuda.current_stream  # launches go to the stream current at call time
     C = torch.empty((M, N), dtype=torch.float32, device="cuda")
     P = {"name": name, "M": M, "K": A.num_cols, "N": N, "nnz": A.nnz, "host": A, "B": B,
          "desc": desc, "backend": plan.backend_name, "C": C,
@@ -132,7 +136,7 @@ def build_pattern(S, torch, name: str):
         dA = S.DeviceBSR(hb)
         B16 = S.float_to_half(torch.from_numpy(B).cuda())
         P.update(host_bsr=hb, blocks=hb.num_blocks, form="wmma", dtype="f16 in, f32 accumulate")
-        P["launch"] = lambda reps: S.launch_repeat("wmma", dA, B16, C, reps, stream)
+        P["launch"] = lambda reps: S.launch_repeat("wmma", dA, B16, C, reps, cur())
         P["keep"] = (dA, B16)
         return P
     form, opts, parts = S.csr_auto_form(A, N)
@@ -143,10 +147,10 @@ def build_pattern(S, torch, name: str):
         rows = torch.from_numpy(S.nnz_split_rows(A, parts)).cuda()
         carry = torch.empty((parts, N), dtype=torch.float32, device="cuda")
         P["parts"] = parts
-        P["launch"] = lambda reps: S.launch_repeat_split(dA, rows, dB, C, carry, reps, stream)
+        P["launch"] = lambda reps: S.launch_repeat_split(dA, rows, dB, C, carry, reps, cur())
         P["keep"] = (dA, dB, rows, carry)
     else:
-        P["launch"] = lambda reps: S.launch_repeat_opts(dA, dB, C, opts, reps, stream)
+        P["launch"] = lambda reps: S.launch_repeat_opts(dA, dB, C, opts, reps, cur())
         P["keep"] = (dA, dB)
     return P
 
@@ -178,6 +182,48 @@ def time_cold(torch, P, flush, reps: int = 15) -> float:
         evs.append((e0, e1))
     torch.cuda.synchronize()
     return _median([a.elapsed_time(b) for a, b in evs])
+
+
+def time_graph(torch, P, launches: int = 100, replays: int = 10):
+    """Per-launch time when `launches` back-to-back launches are captured in
+    one HIP graph and replayed (the device-side floor without the host's
+    per-launch cost); also checks that a replay leaves the same C, bit for
+    bit, as the eager launches.  Returns (ms, None) or (None, reason)."""
+    C = P["C"]
+    torch.cuda.synchronize()
+    P["launch"](1)
+    torch.cuda.synchronize()
+    want = C.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        P["launch"](1)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    try:
+        with torch.cuda.graph(g):
+            P["launch"](launches)
+    except Exception as e:  # capture refused: report, keep the eager figures
+        torch.cuda.synchronize()
+        return None, f"capture failed: {e}"[:200]
+    C.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(C.view(torch.int32), want.view(torch.int32)):
+        return None, "replay differs from the eager launches"
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    g.replay()
+    e0.record(stream)
+    for _ in range(replays):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (replays * launches)
+    del g
+    return ms, None
 
 
 def pattern_block(P, ms: float, cold_ms: float):
@@ -255,6 +301,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache timings")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="skip the graph-replay timings (graph_ms_per_step)")
     ap.add_argument("--only", default="",
                     help="comma-separated subset of c1..c5 (profiling runs); the headline "
                          "line needs c2")
@@ -287,6 +335,11 @@ def main() -> int:
         ms = time_warm(torch, P, args.steps, args.warmup)
         cold = time_cold(torch, P, flush) if flush is not None else None
         blk, flops = pattern_block(P, ms, cold)
+        if not args.no_graph:
+            gms, why = time_graph(torch, P)
+            blk["graph_ms_per_step"] = None if gms is None else round(gms, 6)
+            if why:
+                blk["graph_note"] = why
         if not args.no_cpu:
             blk["cpu_baseline"] = cpu_baseline(P, flops)
         blocks[name] = blk

@@ -289,6 +289,28 @@ def test_wmma_c_alignment(S, O, torch):
         check_bsr(a, C32, absC)
 
 
+@pytest.mark.parametrize("N", [8, 24, 40, 72])
+def test_wmma_partial_column_tiles(S, O, torch, N):
+    # N % 8 == 0 but not a multiple of the 16 * tiles columns a wave covers:
+    # the record kernel's 16-byte row-chunk C stores skip the chunks past N
+    # (rows past M too: M = 45 leaves a partial last block-row)
+    rng = np.random.default_rng(40 + N)
+    A = S.generate_uniform_random_csr(45, 70, 0.1, 9)
+    A.values = S.round_to_fp16(A.values)
+    B = S.round_to_fp16(rng.uniform(-1, 1, (70, N)).astype(np.float32))
+    hb, B16, C32, C64, absC = _refs(S, O, A, B)
+    dA = S.DeviceBSR(hb)
+    dB = torch.from_numpy(B16.view(np.int16)).cuda()
+    for tiles in (1, 2, 4):
+        say(f"wmma partial tiles N={N} tiles={tiles}")
+        C = torch.full((45, N), float("nan"), device="cuda")
+        S.spmm_wmma_opts(dA, dB, S.BsrOptsT(1, tiles, 0, 2), C)
+        torch.cuda.synchronize()
+        got = C.cpu().numpy()
+        check_bsr(got, C32, absC)
+        check_csr(got, C64, absC, tol=1e-5)
+
+
 def test_wmma_bad_row_group(S, torch):
     A = S.generate_banded_csr(64, 64, 3, 1)
     dA = S.DeviceBSR(S.bsr_from_csr_host(A))

@@ -10,8 +10,10 @@ hint, sub-wave row groups, or the merge-path partition).
 
 One step = one pass of the hot path over inputs already resident in HBM
 (for the merge-path form: its engine launch plus its carry fix-up).  W untimed
-steps, then K steps back to back on torch's current stream between two events
-on that stream, synchronised on both sides.  `cold_ms_median` is the median of
+steps (by default at least 50 and for at least 0.1 s, until the rate is
+steady; `warmup` reports the count), then K steps back to back on torch's
+current stream between two events on that stream, synchronised on both
+sides.  `cold_ms_median` is the median of
 single launches each preceded by a 512 MiB write that evicts L2 (4 MiB per
 XCD) and the 256 MB MALL; warm is the contract figure.  `graph_ms_per_step`
 is the same launches captured 100 at a time in one HIP graph and replayed (a
@@ -45,6 +47,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E datasheet
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA datasheet
 COPY_BYTES = 256 * 1024 * 1024
 FLUSH_BYTES = 512 * 1024 * 1024
+WARM_S = 0.1  # seconds of untimed launches before timing, when --warmup is not given
 METRIC = "SpMM GFLOP/s (2*nnz*N/t) + % HBM/MFMA roofline, m=8192 per pattern"
 HEADLINE = "c2"
 ORDER = ("c1", "c2", "c3", "c4", "c5")
@@ -155,10 +158,28 @@ def build_pattern(S, torch, name: str):
     return P
 
 
-def time_warm(torch, P, steps: int, warmup: int) -> float:
-    stream = torch.cuda.current_stream()
-    P["launch"](max(warmup, 1))
+def warm_up(torch, P, warmup, warm_s: float = WARM_S, chunk: int = 200) -> int:
+    """Untimed launches before the timed ones: exactly `warmup` if given, else
+    at least 50 and for at least `warm_s` seconds.  c2 needs about 2000
+    launches to reach its steady rate (18.1 us per step after 50, 17.6 after
+    500, 17.1 after 2000); c3 and c5 change by under 1%.  Returns the count."""
+    if warmup is not None:
+        P["launch"](max(warmup, 1))
+        torch.cuda.synchronize()
+        return max(warmup, 1)
+    done = 50
+    t0 = time.perf_counter()
+    P["launch"](done)
     torch.cuda.synchronize()
+    while time.perf_counter() - t0 < warm_s:
+        P["launch"](chunk)
+        torch.cuda.synchronize()
+        done += chunk
+    return done
+
+
+def time_warm(torch, P, steps: int) -> float:
+    stream = torch.cuda.current_stream()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
@@ -298,7 +319,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed launches per pattern (default: at least 50 and for at "
+                         "least 0.1 s, until the rate is steady)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-cold", action="store_true", help="skip the cold-cache timings")
     ap.add_argument("--no-graph", action="store_true",
@@ -332,9 +355,11 @@ def main() -> int:
     blocks = {}
     for name in names:
         P = build_pattern(S, torch, name)
-        ms = time_warm(torch, P, args.steps, args.warmup)
+        warmed = warm_up(torch, P, args.warmup)
+        ms = time_warm(torch, P, args.steps)
         cold = time_cold(torch, P, flush) if flush is not None else None
         blk, flops = pattern_block(P, ms, cold)
+        blk["warmup_steps"] = warmed
         if not args.no_graph:
             gms, why = time_graph(torch, P)
             blk["graph_ms_per_step"] = None if gms is None else round(gms, 6)
@@ -367,7 +392,7 @@ def main() -> int:
         "unit": "GFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": h["warmup_steps"],
         "ms_per_step": h["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",

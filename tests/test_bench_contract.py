@@ -91,3 +91,22 @@ def test_roofline_units(backend):
         assert r["hbm"]["alg_bytes"] == 516 * 8192 + 4 * 513 + 2 * 8192 * 256 + 4 * 8192 * 256
         assert r["frac"] == pytest.approx(r["exec_flops"] / (ms * 1e-3) / 2.5e15, abs=1e-4)
         assert blk["cold_ms_median"] == 0.012
+
+
+def test_warm_up_counts():
+    # an explicit --warmup is honoured exactly; the default warms for at least
+    # 50 launches and WARM_S seconds and reports how many it ran
+    class _Cuda:
+        @staticmethod
+        def synchronize():
+            pass
+
+    class _Torch:
+        cuda = _Cuda()
+
+    calls = []
+    P = {"launch": lambda n: calls.append(n)}
+    assert bench.warm_up(_Torch(), P, 7) == 7 and calls == [7]
+    calls.clear()
+    done = bench.warm_up(_Torch(), P, None, warm_s=0.02, chunk=10)
+    assert done == sum(calls) and done >= 50 and calls[0] == 50

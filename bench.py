@@ -6,10 +6,12 @@ the configuration the metric is quoted on; `patterns` holds one block per
 BASELINE config (c1 .. c5), each timed the way spmm_hybrid_run runs it: the
 backend hybrid_choose picks (reference spmm_hybrid.cu:32-56), and for CSR the
 form the hybrid's CSR branch picks (row-block engine with the longest row as
-hint, sub-wave row groups, or the merge-path partition).
+hint, sub-wave row groups, the merge-path partition, or the merge-path
+partition over B-row halves).
 
 One step = one pass of the hot path over inputs already resident in HBM
-(for the merge-path form: its engine launch plus its carry fix-up).  W untimed
+(for the merge-path forms: the engine launch plus its fix-up; the B-row
+halves' plan, built once from the host matrix, is outside the timed steps).  W untimed
 steps (by default at least 50 and for at least 0.1 s, until the rate is
 steady; `warmup` reports the count), then K steps back to back on torch's
 current stream between two events on that stream, synchronised on both
@@ -143,9 +145,14 @@ def build_pattern(S, torch, name: str):
         P["keep"] = (dA, B16)
         return P
     form, opts, parts = S.csr_auto_form(A, N)
-    dA = S.DeviceCSR(A)
     dB = torch.from_numpy(B).cuda()
     P.update(form=form, dtype="f32")
+    if form == "khalf":
+        kp = S.KHalfPlan(A, N)
+        P["launch"] = lambda reps: kp.launch_repeat(dB, C, reps, cur())
+        P["keep"] = (kp, dB)
+        return P
+    dA = S.DeviceCSR(A)
     if form == "split":
         rows = torch.from_numpy(S.nnz_split_rows(A, parts)).cuda()
         carry = torch.empty((parts, N), dtype=torch.float32, device="cuda")

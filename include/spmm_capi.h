@@ -234,12 +234,39 @@ int spmm_c_tiled_v3_split_noalloc(const spmm_csr_t* d_A, const int* d_split_rows
                                   const float* d_B, float* d_C, int N, void* stream);
 /* The CSR form spmm_hybrid_run's CSR branch picks for host CSR h and a B of N
  * columns (no counterpart in the reference): *form_out = 0 the row-block
- * engine, 1 sub-wave row groups, 2 the merge-path partition; *opts_out the
- * launch options for spmm_c_tiled_v3_opts (forms 0 and 1: the longest row as
- * max_row_hint, row_groups = 1 for form 1); *parts_out the merge-path parts
- * (form 2, else 0).  Host only. */
+ * engine, 1 sub-wave row groups, 2 the merge-path partition, 3 the merge-path
+ * partition over B-row halves (spmm_c_khalf_*); *opts_out the launch options
+ * for spmm_c_tiled_v3_opts (forms 0 and 1: the longest row as max_row_hint,
+ * row_groups = 1 for form 1); *parts_out the merge-path parts (form 2, else
+ * 0).  Host only. */
 int spmm_c_csr_auto_form(const spmm_csr_t* h, int N, int* form_out,
                          spmm_engine_opts_t* opts_out, int* parts_out);
+/* Merge-path partition over B-row halves (no counterpart in the reference;
+ * spmm_hybrid_run's CSR form when B is over one XCD's 4 MiB L2 at full width
+ * and half of its rows fit, form 3 above).  A's entries with column < K/2 and
+ * the rest each get their own merge-path partition; XCDs 0-3 multiply the
+ * first half by B rows [0, K/2) and XCDs 4-7 the second by rows [K/2, K), each
+ * over all N columns; a second kernel adds the halves' carries and the second
+ * half's partial rows to C in a fixed order (deterministic).
+ * create: h_A is a host CSR with columns in [0, num_cols); uploads both halves
+ *   and allocates the plan's workspaces (an M x N partial, parts x N carries
+ *   per half).  SPMM_UNSUPPORTED unless N % 4 == 0, num_cols x N x 4 bytes is
+ *   over 4 MiB with half of the rows within it (and N x 4 <= 16383, B within
+ *   2 GiB), and each half holds at least 512 entries.
+ * launch: d_B (num_cols x N, the N given to create) and d_C (M x N), fp32,
+ *   16-byte aligned; two kernels on `stream`; the plan's workspaces are shared by its launches, so
+ *   launches of one plan must not overlap.
+ * runs: host helper behind the fix-up's per-row carry table -- for the
+ *   merge-path partition of row_ptr (M rows, nnz entries) into parts with row
+ *   table split_rows, first[r] / last[r] = the first and last part continuing
+ *   row r (whose first nonzero lies in an earlier part), -1 when none. */
+typedef struct spmm_khalf_plan spmm_khalf_plan_t;
+int  spmm_c_khalf_plan_create(const spmm_csr_t* h_A, int N, spmm_khalf_plan_t** plan_out);
+int  spmm_c_khalf_launch(const spmm_khalf_plan_t* plan, const float* d_B, float* d_C,
+                         void* stream);
+void spmm_c_khalf_plan_destroy(spmm_khalf_plan_t* plan);
+int  spmm_c_khalf_runs(const int* row_ptr, int M, long long nnz, const int* split_rows,
+                       int parts, int* first_out, int* last_out);
 /* spmm_tiled_v3 with explicit engine options (no reference counterpart). */
 int spmm_c_tiled_v3_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
                          const spmm_engine_opts_t* opts, void* stream);
@@ -286,6 +313,8 @@ int spmm_c_launch_repeat_split(const spmm_csr_t* d_A, const int* d_split_rows, i
                                void* stream);
 int spmm_c_launch_repeat_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
                               const spmm_engine_opts_t* opts, int reps, void* stream);
+int spmm_c_launch_repeat_khalf(const spmm_khalf_plan_t* plan, const float* d_B, float* d_C,
+                               int reps, void* stream);
 /* Same for the matrix-core kernel with explicit options. */
 int spmm_c_launch_repeat_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B_fp16,
                                    float* d_C, int N, const spmm_bsr_opts_t* opts, int reps,

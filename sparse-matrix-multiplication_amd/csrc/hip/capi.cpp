@@ -610,17 +610,60 @@ int spmm_c_csr_auto_form(const spmm_csr_t* h, int N, int* form_out, spmm_engine_
     if (h == nullptr || form_out == nullptr || opts_out == nullptr || parts_out == nullptr) {
         return set_error(SPMM_INVALID, "null argument");
     }
-    if (N < 0 || h->num_rows < 0 || h->nnz < 0 || (h->num_rows > 0 && h->row_ptr == nullptr)) {
+    if (N < 0 || h->num_rows < 0 || h->nnz < 0 || (h->num_rows > 0 && h->row_ptr == nullptr) ||
+        (h->nnz > 0 && h->col_idx == nullptr)) {
         return set_error(SPMM_INVALID, "bad CSR or N");
     }
     const spmm::engine::CsrChoice ch = spmm::engine::choose_csr_form(to_cpp(*h), N);
     *form_out  = ch.form == spmm::engine::CsrForm::RowGroups ? 1
                  : ch.form == spmm::engine::CsrForm::Split   ? 2
+                 : ch.form == spmm::engine::CsrForm::KHalf   ? 3
                                                              : 0;
     *opts_out  = spmm_engine_opts_t{};
     opts_out->row_groups   = ch.opts.row_groups;
     opts_out->max_row_hint = ch.opts.max_row_hint;
     *parts_out = ch.parts;
+    return ok();
+}
+
+struct spmm_khalf_plan {
+    spmm::engine::KHalfPlan p;
+};
+
+int spmm_c_khalf_plan_create(const spmm_csr_t* h_A, int N, spmm_khalf_plan_t** plan_out) {
+    if (h_A == nullptr || plan_out == nullptr) return set_error(SPMM_INVALID, "null argument");
+    *plan_out = nullptr;
+    spmm_khalf_plan_t* plan = new (std::nothrow) spmm_khalf_plan_t;
+    if (plan == nullptr) return set_error(SPMM_INVALID, "out of host memory");
+    const int rc = from_engine(spmm::engine::khalf_plan_build(to_cpp(*h_A), N, &plan->p));
+    if (rc != SPMM_OK) {
+        delete plan;
+        return rc;
+    }
+    *plan_out = plan;
+    return ok();
+}
+
+int spmm_c_khalf_launch(const spmm_khalf_plan_t* plan, const float* d_B, float* d_C,
+                        void* stream) {
+    if (plan == nullptr) return set_error(SPMM_INVALID, "null plan");
+    return from_engine(spmm::engine::launch_csr_khalf(plan->p, d_B, d_C, as_stream(stream)));
+}
+
+void spmm_c_khalf_plan_destroy(spmm_khalf_plan_t* plan) {
+    if (plan == nullptr) return;
+    spmm::engine::khalf_plan_free(&plan->p);
+    delete plan;
+}
+
+int spmm_c_khalf_runs(const int* row_ptr, int M, long long nnz, const int* split_rows, int parts,
+                      int* first_out, int* last_out) {
+    if (M < 0 || nnz < 0 || parts < 1) return set_error(SPMM_INVALID, "bad size");
+    if ((M > 0 && (row_ptr == nullptr || first_out == nullptr || last_out == nullptr)) ||
+        split_rows == nullptr) {
+        return set_error(SPMM_INVALID, "null argument");
+    }
+    spmm::engine::khalf_runs(row_ptr, M, nnz, split_rows, parts, first_out, last_out);
     return ok();
 }
 
@@ -761,6 +804,17 @@ int spmm_c_launch_repeat_opts(const spmm_csr_t* d_A, const float* d_B, float* d_
     for (int i = 0; i < reps; ++i) {
         const int rc = from_engine(spmm::engine::launch_csr(
             spmm::engine::CsrRole::TiledV3, A, d_B, d_C, N, as_stream(stream), nullptr, 0, &o));
+        if (rc != SPMM_OK) return rc;
+    }
+    return ok();
+}
+
+int spmm_c_launch_repeat_khalf(const spmm_khalf_plan_t* plan, const float* d_B, float* d_C,
+                               int reps, void* stream) {
+    if (plan == nullptr) return set_error(SPMM_INVALID, "null plan");
+    for (int i = 0; i < reps; ++i) {
+        const int rc = from_engine(
+            spmm::engine::launch_csr_khalf(plan->p, d_B, d_C, as_stream(stream)));
         if (rc != SPMM_OK) return rc;
     }
     return ok();

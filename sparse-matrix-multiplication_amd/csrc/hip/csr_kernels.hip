@@ -171,6 +171,21 @@ struct RowblockArgs {
     const int*   split_rows;
     float*       carry;
     long long    nnz;
+    // B-row halves (merge-path only): workgroups on XCDs 4-7 take this second
+    // descriptor -- the entries of A whose columns lie in B's upper rows, with
+    // rebased columns, those B rows, their own output and merge-path table --
+    // and XCDs 0-3 the first, so each XCD's L2 holds half of B at full width.
+    int          halves = 0;
+    const int*   row_ptr1 = nullptr;
+    const int*   col_idx1 = nullptr;
+    const float* vals1 = nullptr;
+    const float* B1 = nullptr;
+    float*       C1 = nullptr;
+    int          K1 = 0;
+    const int*   split_rows1 = nullptr;
+    float*       carry1 = nullptr;
+    long long    nnz1 = 0;
+    int          nblocks1 = 0;
 };
 
 constexpr int kRpCap = 1024;  // row pointers staged per window
@@ -253,9 +268,26 @@ __global__ __launch_bounds__(WAVES * 64) void csr_rowblock(RowblockArgs a) {
     // Column slices are tied to XCDs: workgroups are dispatched round-robin
     // over the 8 XCDs, so workgroup g runs on XCD g % 8.  With S slices, XCDs
     // s*8/S .. (s+1)*8/S - 1 compute columns [s*SC, (s+1)*SC) of every row
-    // block, so each XCD's L2 holds only 1/S of B.
+    // block, so each XCD's L2 holds only 1/S of B.  With B-row halves, XCDs
+    // 0-3 work through the parts of the first descriptor and XCDs 4-7 through
+    // those of the second (all columns each).
     int rb = blockIdx.x, slice = 0;
-    if (a.slices > 1) {
+    if (a.halves) {
+        const int x = blockIdx.x & 7;
+        rb = (blockIdx.x >> 3) * 4 + (x & 3);
+        if (x >= 4) {
+            a.row_ptr    = a.row_ptr1;
+            a.col_idx    = a.col_idx1;
+            a.vals       = a.vals1;
+            a.B          = a.B1;
+            a.C          = a.C1;
+            a.K          = a.K1;
+            a.split_rows = a.split_rows1;
+            a.carry      = a.carry1;
+            a.nnz        = a.nnz1;
+            a.nblocks    = a.nblocks1;
+        }
+    } else if (a.slices > 1) {
         const int per = 8 / a.slices;  // XCDs per slice
         const int x   = blockIdx.x & 7;
         rb    = (blockIdx.x >> 3) * per + x % per;
@@ -537,6 +569,52 @@ __global__ __launch_bounds__(64) void csr_split_fixup(const int* __restrict__ ro
             const int c = c0 + lane + 64 * j;
             if (c < N) crow[c] = cv[j] + s[j];
         }
+    }
+}
+
+// Fix-up of the B-row halves: C = (C + carries of half 0) + (partial +
+// carries of half 1), row by row, each sum of carries in part order --
+// the same order on every launch.  runs[r] = (first, last) continuation part
+// of row r in half 0, then in half 1, -1 for none.  C and partial are walked as
+// flat 16-byte chunks (N % 4 == 0), two per thread, loads issued before use.
+__global__ __launch_bounds__(256) void csr_khalf_fixup(float* __restrict__ C,
+                                                       const float* __restrict__ partial,
+                                                       const float* __restrict__ carry0,
+                                                       const float* __restrict__ carry1,
+                                                       const int4* __restrict__ runs, int N,
+                                                       long long chunks) {
+    const long long t0 = static_cast<long long>(blockIdx.x) * 512 + threadIdx.x;
+    f32x4 cv[2], pv[2];
+    int4  ru[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const long long t = t0 + 256 * k;
+        if (t < chunks) {
+            ru[k] = runs[t * 4 / N];
+            cv[k] = reinterpret_cast<const f32x4*>(C)[t];
+            pv[k] = reinterpret_cast<const f32x4*>(partial)[t];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const long long t = t0 + 256 * k;
+        if (t >= chunks) continue;
+        const int c = static_cast<int>(t * 4 % N);
+        if (ru[k].x >= 0) {
+            f32x4 s = f32x4(0.f);
+            for (int p = ru[k].x; p <= ru[k].y; ++p) {
+                s += *reinterpret_cast<const f32x4*>(carry0 + static_cast<size_t>(p) * N + c);
+            }
+            cv[k] += s;
+        }
+        if (ru[k].z >= 0) {
+            f32x4 s = f32x4(0.f);
+            for (int p = ru[k].z; p <= ru[k].w; ++p) {
+                s += *reinterpret_cast<const f32x4*>(carry1 + static_cast<size_t>(p) * N + c);
+            }
+            pv[k] += s;
+        }
+        __builtin_nontemporal_store(cv[k] + pv[k], reinterpret_cast<f32x4*>(C) + t);
     }
 }
 
@@ -1257,6 +1335,59 @@ Error launch_csr_split(const CSR& A, const float* B, float* C, int N, hipStream_
         return fail(kInvalid, "split partition needs a carry workspace of parts x N floats");
     }
     return launch_csr_impl(CsrRole::TiledV3, A, B, C, N, stream, nullptr, 0, opts, &plan);
+}
+
+bool khalf_pays(int K, int N) {
+    // B over one XCD's 4 MiB L2 at full width, its half of the rows within it.
+    // Measured on MI355X on c5 (16384^2 power-law, N = 128, B 8 MiB): the
+    // merge-path engine 63.9 -> 55.0 us with each half's B rows resident in
+    // its four XCDs' L2s, the fix-up 4.8 -> 6.7 us (it now also adds the
+    // second half's partial C), 67.8 -> 61.7 us per launch.
+    const long long row_bytes = static_cast<long long>(N) * 4;
+    return N > 0 && N % 4 == 0 && K >= 2 && b_fits_buffer(K, N) &&
+           static_cast<long long>(K) * row_bytes > (4LL << 20) &&
+           static_cast<long long>((K + 1) / 2) * row_bytes <= (4LL << 20);
+}
+
+Error launch_csr_khalf(const KHalfPlan& p, const float* B, float* C, hipStream_t stream) {
+    if (p.M < 0 || p.N < 0) return fail(kInvalid, "negative matrix dimension");
+    if (p.M == 0 || p.N == 0) return ok();
+    if (B == nullptr || C == nullptr || p.partial == nullptr || p.runs == nullptr) {
+        return fail(kInvalid, "null device pointer");
+    }
+    if (p.N % 4 != 0 || !aligned(B, 16) || !aligned(C, 16)) {
+        return fail(kUnsupported, "B-row halves need N % 4 == 0 and 16-byte aligned B and C");
+    }
+    for (int h = 0; h < 2; ++h) {
+        if (p.parts[h] < 1 || p.parts[h] > std::max(p.half[h].nnz, 1) || p.rows[h] == nullptr ||
+            p.carry[h] == nullptr) {
+            return fail(kInvalid, "B-row halves: incomplete plan");
+        }
+    }
+    const int N = p.N;
+    RowblockArgs args{p.half[0].row_ptr, p.half[0].col_idx, p.half[0].values, B, C, nullptr,
+                      p.M, N, p.K0, 0, p.parts[0], 1, N, p.rows[0], p.carry[0], p.half[0].nnz};
+    args.halves      = 1;
+    args.row_ptr1    = p.half[1].row_ptr;
+    args.col_idx1    = p.half[1].col_idx;
+    args.vals1       = p.half[1].values;
+    args.B1          = B + static_cast<size_t>(p.K0) * N;
+    args.C1          = p.partial;
+    args.K1          = p.K - p.K0;
+    args.split_rows1 = p.rows[1];
+    args.carry1      = p.carry[1];
+    args.nnz1        = p.half[1].nnz;
+    args.nblocks1    = p.parts[1];
+    const int grid   = 8 * ceil_div(std::max(p.parts[0], p.parts[1]), 4);
+    hipError_t e = dispatch_groups<4>(pick_groups(N, 4, 0), 4, 4, true, args, grid, stream);
+    if (e == hipSuccess) {
+        const long long chunks = static_cast<long long>(p.M) * N / 4;
+        hipLaunchKernelGGL(csr_khalf_fixup, dim3(static_cast<unsigned>((chunks + 511) / 512)),
+                           dim3(256), 0, stream, C, p.partial, p.carry[0], p.carry[1],
+                           reinterpret_cast<const int4*>(p.runs), N, chunks);
+        e = hipGetLastError();
+    }
+    return from_hip(e, "csr B-row halves launch");
 }
 
 }  // namespace engine

@@ -136,6 +136,38 @@ Error launch_csr_split(const CSR& d_A, const float* d_B, float* d_C, int N, hipS
 Error launch_csr_split_noalloc(const CSR& d_A, const int* d_split_rows, int parts,
                                const float* d_B, float* d_C, int N, hipStream_t stream);
 long noalloc_scratch_floats();
+
+// B-row halves of the merge-path launch, for a B over one XCD's 4 MiB L2 at
+// full width whose half fits (khalf_pays).  A's entries with column < K0 =
+// K/2 form half 0, the rest (columns rebased by K0) half 1, each with its own
+// merge-path partition.  One launch runs half 0 on XCDs 0-3 into C and half 1
+// on XCDs 4-7 into `partial`, all N columns each, so every XCD's L2 holds
+// half of B's rows at full width; a second kernel adds, row by row, half 0's
+// carries to C and half 1's to the partial, then the partial to C (a fixed
+// order: deterministic).  Built once from the host matrix, reused for any B
+// of N columns; device memory is owned by the plan (khalf_plan_free).
+struct KHalfPlan {
+    CSR    half[2]  = {};       // device
+    int*   rows[2]  = {};       // merge-path row tables, parts + 1 ints each
+    int    parts[2] = {};
+    float* carry[2] = {};       // parts x N floats each
+    float* partial  = nullptr;  // M x N floats: half 1's rows
+    int*   runs     = nullptr;  // M x 4 ints: (first, last) carry part of each row in
+                                // half 0, then in half 1; -1 for none
+    int    M = 0, K = 0, K0 = 0, N = 0;
+};
+bool  khalf_pays(int K, int N);
+// Host CSR in (columns in [0, K)); kUnsupported unless khalf_pays(K, N) and
+// each half holds at least kKHalfMinNnz entries.
+constexpr int kKHalfMinNnz = 512;
+Error khalf_plan_build(const CSR& h_A, int N, KHalfPlan* out);
+void  khalf_plan_free(KHalfPlan* p);
+Error launch_csr_khalf(const KHalfPlan& p, const float* d_B, float* d_C, hipStream_t stream);
+// For a merge-path partition (row_ptr of M rows, nnz entries, split_rows of
+// parts + 1): first[r] / last[r] = the first and last part that continues row
+// r (its first nonzero lies in an earlier part), -1 when none.
+void khalf_runs(const int* row_ptr, int M, long long nnz, const int* split_rows, int parts,
+                int* first, int* last);
 // Parts of the merge-path partition for nnz nonzeros, and whether it beats
 // the row partition for a matrix whose longest row has max_row_nnz entries.
 int split_partition_parts(int nnz);
@@ -151,17 +183,19 @@ int default_partition_parts(int num_rows, int nnz);
 // The CSR form spmm_hybrid_run's CSR branch runs for a host CSR and a B of N
 // columns, decided from its row lengths: sub-wave row groups when
 // row_groups_pay, the merge-path partition when split_pays (parts from
-// split_partition_parts), the row-block engine otherwise.  opts carries the
-// longest row as max_row_hint (and row_groups = 1 for row groups).
-enum class CsrForm { RowGroups, Engine, Split };
+// split_partition_parts) -- split over B-row halves when khalf_pays and each
+// half holds at least kKHalfMinNnz entries -- the row-block engine
+// otherwise.  opts carries the longest row as max_row_hint (and row_groups =
+// 1 for row groups).
+enum class CsrForm { RowGroups, Engine, Split, KHalf };
 struct CsrChoice {
     CsrForm    form    = CsrForm::Engine;
     EngineOpts opts;
-    int        parts   = 0;  // merge-path parts (Split only)
+    int        parts   = 0;  // merge-path parts (Split only; KHalf plans choose their own)
     int        max_row = 0;
 };
 CsrChoice choose_csr_form(const CSR& h_A, int N);
-const char* csr_form_name(CsrForm f);  // "rowgroups", "engine", "split"
+const char* csr_form_name(CsrForm f);  // "rowgroups", "engine", "split", "khalf"
 
 }  // namespace engine
 }  // namespace spmm

@@ -132,12 +132,32 @@ CsrChoice choose_csr_form(const CSR& h_A, int N) {
     } else if (split_pays(ch.max_row)) {
         ch.form  = CsrForm::Split;
         ch.parts = split_partition_parts(h_A.nnz);
+        if (khalf_pays(h_A.num_cols, N) && h_A.col_idx != nullptr) {
+            // each half needs its share of entries, and every column a half
+            const int K = h_A.num_cols, K0 = K / 2;
+            long long n0 = 0, n1 = 0;
+            bool in_range = true;
+            for (int e = 0; e < h_A.nnz && in_range; ++e) {
+                const int c = h_A.col_idx[e];
+                in_range = c >= 0 && c < K;
+                (c < K0 ? n0 : n1) += 1;
+            }
+            if (in_range && n0 >= kKHalfMinNnz && n1 >= kKHalfMinNnz) {
+                ch.form  = CsrForm::KHalf;
+                ch.parts = 0;
+            }
+        }
     }
     return ch;
 }
 
 const char* csr_form_name(CsrForm f) {
-    return f == CsrForm::RowGroups ? "rowgroups" : (f == CsrForm::Split ? "split" : "engine");
+    switch (f) {
+        case CsrForm::RowGroups: return "rowgroups";
+        case CsrForm::Split: return "split";
+        case CsrForm::KHalf: return "khalf";
+        default: return "engine";
+    }
 }
 
 Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float* h_C, int N,
@@ -187,11 +207,22 @@ Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float
         // the rest, so then the engine runs the merge-path partition instead:
         // equal nonzero ranges per workgroup, long rows cut between them.
         // Narrow B, short rows and tall matrices of even rows, with no long
-        // row, go to the sub-wave row groups (row_groups_pay).
-        DeviceCsrCopy csr;
-        SPMM_TRY(upload_csr(h_A, csr));
+        // row, go to the sub-wave row groups (row_groups_pay).  A merge-path
+        // input whose B outgrows one XCD's L2 at full width, but not at half
+        // its rows, runs over B-row halves (khalf_pays).
         const CsrChoice ch = choose_csr_form(h_A, N);
-        if (ch.form != CsrForm::Split) {
+        DeviceCsrCopy csr;
+        if (ch.form != CsrForm::KHalf) SPMM_TRY(upload_csr(h_A, csr));
+        if (ch.form == CsrForm::KHalf) {
+            struct PlanGuard {
+                KHalfPlan p;
+                ~PlanGuard() { khalf_plan_free(&p); }
+            } g;
+            SPMM_TRY(khalf_plan_build(h_A, N, &g.p));
+            SPMM_TRY(time_median_launch(
+                [&] { return launch_csr_khalf(g.p, d_B.as<float>(), d_C.as<float>(), nullptr); },
+                warmup, iters, ms));
+        } else if (ch.form != CsrForm::Split) {
             // Row groups, or the row-block engine given the longest row (the
             // whole-round grid when rows are even).
             SPMM_TRY(time_median_launch(

@@ -130,6 +130,11 @@ _SIGNATURES = {
     "spmm_c_tiled_v3_split_noalloc": (_int, [_P(CsrT), _vp, _int, _vp, _vp, _int, _vp]),
     "spmm_c_launch_repeat_split": (_int, [_P(CsrT), _vp, _int, _vp, _vp, _int, _vp, _int, _vp]),
     "spmm_c_default_partition_parts": (_int, [_int, _int]),
+    "spmm_c_khalf_plan_create": (_int, [_P(CsrT), _int, _P(_vp)]),
+    "spmm_c_khalf_launch": (_int, [_vp, _vp, _vp, _vp]),
+    "spmm_c_khalf_plan_destroy": (None, [_vp]),
+    "spmm_c_khalf_runs": (_int, [_vp, _int, ctypes.c_longlong, _vp, _int, _vp, _vp]),
+    "spmm_c_launch_repeat_khalf": (_int, [_vp, _vp, _vp, _int, _vp]),
     "spmm_c_csr_auto_form": (_int, [_P(CsrT), _int, _P(ctypes.c_int),
                                     _P(EngineOptsT), _P(ctypes.c_int)]),
     "spmm_c_tiled_v3_opts": (_int, [_P(CsrT), _vp, _vp, _int, _P(EngineOptsT), _vp]),
@@ -409,7 +414,7 @@ def split_partition_parts(nnz: int) -> int:
     return int(lib().spmm_c_split_partition_parts(nnz))
 
 
-_CSR_FORMS = {0: "engine", 1: "rowgroups", 2: "split"}
+_CSR_FORMS = {0: "engine", 1: "rowgroups", 2: "split", 3: "khalf"}
 
 
 def csr_auto_form(m: HostCSR, N: int):
@@ -732,6 +737,77 @@ def spmm_tiled_v3_split_noalloc(A: DeviceCSR, split_rows, B, C=None, stream=None
                                                B.data_ptr(), C.data_ptr(), N,
                                                _stream_handle(stream)))
     return C
+
+
+class KHalfPlan:
+    """Merge-path launch over B-row halves (no counterpart in the reference; the
+    CSR form "khalf" spmm_hybrid_run picks when B is over one XCD's 4 MiB L2 at
+    full width and half of its rows fit).  Built once from a host CSR for B of
+    N columns; owns its device copies of the two halves and its workspaces
+    (release with close(), or use it as a context manager).  Launches of one
+    plan share those workspaces and must not overlap."""
+
+    def __init__(self, A: "HostCSR", N: int):
+        _torch()  # the HIP runtime comes in through torch first
+        self.num_rows, self.num_cols, self.N = A.num_rows, A.num_cols, int(N)
+        handle = ctypes.c_void_p()
+        src = A.struct()
+        _check(lib().spmm_c_khalf_plan_create(ctypes.byref(src), self.N, ctypes.byref(handle)))
+        self._h = handle
+
+    def _operands(self, B, C):
+        torch = _torch()
+        _check_dense(B, "B", (torch.float32,), rows=self.num_cols, cols=self.N)
+        if C is None:
+            C = torch.empty((self.num_rows, self.N), dtype=torch.float32, device=B.device)
+        else:
+            _check_dense(C, "C", (torch.float32,), rows=self.num_rows, cols=self.N,
+                         device=B.device)
+        if self._h is None:
+            raise SpmmError(SPMM_INVALID, "plan is closed")
+        return C
+
+    def launch(self, B, C=None, stream=None):
+        C = self._operands(B, C)
+        _check(lib().spmm_c_khalf_launch(self._h, B.data_ptr(), C.data_ptr(),
+                                         _stream_handle(stream)))
+        return C
+
+    def launch_repeat(self, B, C, reps: int, stream=None) -> None:
+        """reps back-to-back launches (measurement helper)."""
+        C = self._operands(B, C)
+        _check(lib().spmm_c_launch_repeat_khalf(self._h, B.data_ptr(), C.data_ptr(), reps,
+                                                _stream_handle(stream)))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None:
+            lib().spmm_c_khalf_plan_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def khalf_runs(row_ptr, nnz: int, split_rows):
+    """Host helper of the B-row halves fix-up: per row, the first and last
+    merge-path part continuing it (-1 when none) -> (first, last) int32 arrays."""
+    rp = np.ascontiguousarray(row_ptr, np.int32)
+    rows = np.ascontiguousarray(split_rows, np.int32)
+    M = rp.size - 1
+    first = np.empty(max(M, 0), np.int32)
+    last = np.empty(max(M, 0), np.int32)
+    _check(lib().spmm_c_khalf_runs(_ptr(rp), M, int(nnz), _ptr(rows), rows.size - 1,
+                                   _ptr(first), _ptr(last)))
+    return first, last
 
 
 def launch_repeat_split(A: DeviceCSR, split_rows, B, C, carry, reps: int, stream=None) -> None:

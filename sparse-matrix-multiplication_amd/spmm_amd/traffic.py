@@ -7,8 +7,8 @@ directories: FETCH_SIZE and WRITE_SIZE over `bench.py --only <cfg> --no-cold
 268435456 bytes per launch).  Each engine counter (KiB per dispatch) is scaled
 by known bytes / what the counter reads for the copy, then FETCH + WRITE gives
 HBM bytes per launch.  The engine kernels of one step are the spmm:: kernels
-dispatched once per step (the merge-path form has two: the engine and its
-carry fix-up), so set-up kernels dispatched once per run are left out.
+dispatched once per step (the merge-path forms have two: the engine and its
+fix-up), so set-up kernels dispatched once per run are left out.
 
 The JSON records the hash of the kernel sources that decide what the launch
 runs (`sources_sha256`); bench.py publishes the figure only while the current
@@ -32,7 +32,7 @@ COPY_BYTES = 256 * 1024 * 1024
 
 # Source files whose text decides what a pattern's launch runs, per backend.
 SOURCES = {
-    "csr": ("csr_kernels.hip", "hybrid.cpp"),
+    "csr": ("csr_kernels.hip", "hybrid.cpp", "khalf.cpp"),
     "wmma": ("bsr_kernels.hip",),
 }
 

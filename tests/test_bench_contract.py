@@ -27,7 +27,7 @@ def test_more_than_one_gpu_is_refused():
 def test_committed_traffic_matches_current_sources():
     # every pattern's capture is current: same source hash, same form
     forms = {"c1": ("csr", "rowgroups"), "c2": ("csr", "engine"), "c3": ("wmma", "wmma"),
-             "c4": ("wmma", "wmma"), "c5": ("csr", "split")}
+             "c4": ("wmma", "wmma"), "c5": ("csr", "khalf")}
     for name, (backend, form) in forms.items():
         value, note = bench.load_traffic(name, backend, form)
         assert value is not None, f"{name}: {note}"
@@ -47,6 +47,7 @@ def test_stale_traffic_is_not_published(tmp_path, monkeypatch):
     (prof / "traffic_c2.json").write_text(json.dumps(t_stale))
     value, note = bench.load_traffic("c2", "csr", "engine")
     assert value is None and note.startswith("stale")
+    t = dict(t, sources_sha256=traffic.sources_sha256("csr"))  # current sources
     (prof / "traffic_c2.json").write_text(json.dumps(t))
     value, note = bench.load_traffic("c2", "csr", "split")
     assert value is None and "form" in note

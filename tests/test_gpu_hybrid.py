@@ -52,8 +52,12 @@ def _batch_us(torch, launch, reps=50):
 
 def _csr_auto_launcher(S, torch, A, dB, dC):
     """The CSR form spmm_hybrid_run runs on A (spmm_hybrid.cu:103-116's role):
-    row groups, the engine with the longest row as hint, or merge-path."""
+    row groups, the engine with the longest row as hint, merge-path, or
+    merge-path over B-row halves."""
     form, opts, parts = S.csr_auto_form(A, int(dB.shape[1]))
+    if form == "khalf":
+        kp = S.KHalfPlan(A, int(dB.shape[1]))
+        return form, lambda n: kp.launch_repeat(dB, dC, n)
     dA = S.DeviceCSR(A)
     if form == "split":
         rows = torch.from_numpy(S.nnz_split_rows(A, parts)).cuda()

@@ -252,9 +252,22 @@ def test_csr_auto_form(S):
     assert (form, opts.row_groups, opts.max_row_hint, parts) == ("rowgroups", 1, longest(c1), 0)
     form, opts, parts = S.csr_auto_form(c2, 128)  # 8192 rows of 82: the engine's one round
     assert (form, opts.row_groups, opts.max_row_hint, parts) == ("engine", 0, longest(c2), 0)
-    form, opts, parts = S.csr_auto_form(c5, 128)  # a 4096-entry row: merge-path
-    assert (form, parts) == ("split", S.split_partition_parts(c5.nnz))
+    # a 4096-entry row: merge-path; B of 8 MiB (over one XCD's 4 MiB L2, half of
+    # it within): over B-row halves, which choose their own parts
+    form, opts, parts = S.csr_auto_form(c5, 128)
+    assert (form, parts) == ("khalf", 0)
     assert longest(c5) == 4096
+    assert S.csr_auto_form(c5, 120)[0] == "khalf"   # 7.5 MiB, N % 4 == 0
+    assert S.csr_auto_form(c5, 130)[0] == "split"   # N % 4 != 0
+    assert S.csr_auto_form(c5, 256)[0] == "split"   # half of B is 8 MiB
+    # a long row, but only 100 entries in the upper half of the columns (a
+    # half needs 512): plain merge-path
+    rows = np.r_[np.repeat(np.arange(16384), 12), np.zeros(3000, np.int64)]
+    cols = np.r_[(np.arange(16384 * 12) * 7919) % 8192, np.arange(3000) * 2]
+    cols[:100] += 8192
+    lop = S.csr_from_coo_host(16384, 16384, rows, cols, np.ones(rows.size, np.float32))
+    assert longest(lop) > 2560
+    assert S.csr_auto_form(lop, 128)[0] == "split"
     assert S.csr_auto_form(c2, 16)[0] == "rowgroups"
     assert S.csr_auto_form(c2, 256)[0] == "engine"
     # N = 16: four column lanes take rows up to 16384 / 4 = 4096 entries
@@ -293,3 +306,36 @@ def test_nnz_split_rows_definition(S):
                 assert A.row_ptr[rows[g]] <= p < A.row_ptr[rows[g] + 1]  # the row holds p
     with pytest.raises(S.SpmmError):
         S.nnz_split_rows(S.csr_from_coo_host(4, 4, [], [], []), 3)
+
+
+def test_khalf_runs(S):
+    # Per row, the merge-path parts that continue it (their piece of the row
+    # goes to the carry the B-row halves' fix-up adds).  Checked against a
+    # restatement over entries: part g continues a row exactly when its first
+    # entry and the entry before it belong to the same row.
+    for seed, (M, parts) in enumerate([(2000, 64), (300, 512), (50, 7), (1, 3)]):
+        A = S.generate_power_law_csr(M, M * 4, 40.0, 1.5, 1500, seed + 11)
+        if A.nnz < parts:
+            continue
+        rows = S.nnz_split_rows(A, parts)
+        first, last = S.khalf_runs(A.row_ptr, A.nnz, rows)
+        row_of = np.repeat(np.arange(M), np.diff(A.row_ptr))
+        want_first = np.full(M, -1)
+        want_last = np.full(M, -1)
+        for g in range(parts):
+            lo, hi = A.nnz * g // parts, A.nnz * (g + 1) // parts
+            if lo < hi and lo > 0 and row_of[lo] == row_of[lo - 1]:
+                r = row_of[lo]
+                if want_first[r] < 0:
+                    want_first[r] = g
+                want_last[r] = g
+        assert np.array_equal(first, want_first) and np.array_equal(last, want_last)
+        # a run is a block of consecutive parts, all inside the row
+        for r in np.nonzero(first >= 0)[0]:
+            for g in range(first[r], last[r] + 1):
+                assert row_of[A.nnz * g // parts] == r
+    # a row split over many parts: one long row in the middle
+    A = S.csr_from_coo_host(3, 100, [0] * 5 + [1] * 90 + [2] * 5, list(range(5)) + list(range(90)) +
+                            list(range(5)), np.ones(100, np.float32))
+    first, last = S.khalf_runs(A.row_ptr, A.nnz, S.nnz_split_rows(A, 10))
+    assert first.tolist() == [-1, 1, -1] and last.tolist() == [-1, 9, -1]

@@ -237,13 +237,22 @@ int main(int argc, char** argv) {
 
     if (ks == "csr_auto" || ks == "all") {
         // The CSR form spmm_hybrid_run's CSR branch picks from the row lengths
-        // (row groups, the engine with the longest row as hint, or the
-        // merge-path partition), timed like the kernels above.
+        // (row groups, the engine with the longest row as hint, the
+        // merge-path partition, or merge-path over B-row halves), timed like
+        // the kernels above.
         namespace eng = spmm::engine;
         const eng::CsrChoice ch = eng::choose_csr_form(h_A, N);
         int* d_rows = nullptr;
         float* d_carry = nullptr;
         eng::SplitPlan plan;
+        eng::KHalfPlan khalf;
+        if (ch.form == eng::CsrForm::KHalf) {
+            const eng::Error e = eng::khalf_plan_build(h_A, N, &khalf);
+            if (e.status != eng::kOk) {
+                std::fprintf(stderr, "csr_auto plan failed: %s\n", e.message.c_str());
+                std::exit(EXIT_FAILURE);
+            }
+        }
         if (ch.form == eng::CsrForm::Split) {
             const std::vector<int> rows = spmm::nnz_split_rows(h_A, ch.parts);
             HIP_CHECK(hipMalloc(&d_rows, sizeof(int) * rows.size()));
@@ -256,7 +265,8 @@ int main(int argc, char** argv) {
         }
         auto launch = [&] {
             const eng::Error e =
-                ch.form == eng::CsrForm::Split
+                ch.form == eng::CsrForm::KHalf ? eng::launch_csr_khalf(khalf, d_B, d_C, nullptr)
+                : ch.form == eng::CsrForm::Split
                     ? eng::launch_csr_split(d_A, d_B, d_C, N, nullptr, plan)
                     : eng::launch_csr(eng::CsrRole::TiledV3, d_A, d_B, d_C, N, nullptr, nullptr,
                                       0, &ch.opts);
@@ -275,6 +285,7 @@ int main(int argc, char** argv) {
         results.push_back(r);
         if (d_rows != nullptr) HIP_CHECK(hipFree(d_rows));
         if (d_carry != nullptr) HIP_CHECK(hipFree(d_carry));
+        eng::khalf_plan_free(&khalf);
     }
 
     if (ks == "wmma" || ks == "all") {

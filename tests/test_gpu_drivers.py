@@ -58,17 +58,21 @@ def test_bench_all_kernels_uniform():
     (["--m", "2048", "--k", "2048", "--n", "256", "--density", "0.05"], "engine"),
     (["--m", "3000", "--k", "3000", "--n", "64", "--density", "0.01"], "rowgroups"),
     (["--m", "2048", "--k", "4096", "--n", "128", "--pattern", "power-law", "--mean-deg", "200",
-      "--cap", "4096"], None),
+      "--cap", "4096"], "split"),
+    # B of 6 MiB: over one XCD's L2, half of it within
+    (["--m", "2048", "--k", "12288", "--n", "128", "--pattern", "power-law", "--mean-deg", "200",
+      "--cap", "4096"], "khalf"),
 ])
 def test_bench_csr_auto(args, form):
     # the CSR form the hybrid picks, timed in batches: row groups, the engine
     # with the longest row as hint, or the merge-path partition for rows
-    # longer than 2560 entries
+    # longer than 2560 entries (over B-row halves when B is over 4 MiB and
+    # half of it fits one XCD's L2)
     r = _run([BENCH] + args + ["--kernel", "csr_auto", "--warmup", "1", "--iters", "3",
                                "--batch", "4", "--cpu-reps", "1", "--no-cpu-1t"])
     assert r.returncode == 0, r.stderr
     d = _lines(r.stdout, "kernel=")[0]
-    kinds = {"csr_auto[engine]", "csr_auto[rowgroups]", "csr_auto[split]"}
+    kinds = {"csr_auto[engine]", "csr_auto[rowgroups]", "csr_auto[split]", "csr_auto[khalf]"}
     assert d["kernel"] in kinds
     if form is not None:
         assert d["kernel"] == f"csr_auto[{form}]"

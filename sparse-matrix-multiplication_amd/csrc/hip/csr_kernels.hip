@@ -1330,9 +1330,9 @@ Error launch_csr_split(const CSR& A, const float* B, float* C, int N, hipStream_
 bool khalf_pays(int K, int N) {
     // B over one XCD's 4 MiB L2 at full width, its half of the rows within it.
     // Measured on MI355X on c5 (16384^2 power-law, N = 128, B 8 MiB): the
-    // merge-path engine 63.9 -> 55.0 us with each half's B rows resident in
-    // its four XCDs' L2s, the fix-up 4.8 -> ~5.6 us (it now also adds the
-    // second half's partial C), 67.8 -> ~60.2 us per launch.
+    // merge-path engine 64.0 -> 53.9 us with each half's B rows resident in
+    // its four XCDs' L2s, the fix-up 4.7 -> 6.5 us (it now also adds the
+    // second half's partial C), 67.7 -> 60.1 us per launch.
     const long long row_bytes = static_cast<long long>(N) * 4;
     return N > 0 && N % 4 == 0 && K >= 2 && b_fits_buffer(K, N) &&
            static_cast<long long>(K) * row_bytes > (4LL << 20) &&

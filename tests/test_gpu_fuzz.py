@@ -1,7 +1,7 @@
 """Seeded random parity sweep on cuda:0: random shapes, densities, row-length
-skew and engine options for the CSR engine (row partition, merge-path and the
-sub-wave row groups, the latter also with their own load forms, slices and
-longest-row hints), and random shapes and kernel options for the MFMA BSR
+skew and engine options for the CSR engine (row partition, merge-path, merge-path
+over B-row halves and the sub-wave row groups, the latter also with their own
+load forms, slices and longest-row hints), and random shapes and kernel options for the MFMA BSR
 kernel, each checked against the CPU oracle with the same bars as the other
 GPU tests (fp32 CSR within 1e-5 of the fp64 loop; fp16 BSR within 1e-2 of
 fp32 accumulation and within 1e-5 of the exact product of the fp16
@@ -193,3 +193,50 @@ def test_row_groups_random(S, O, torch, chunk):
         S.spmm_csr("tiled_v3", dA, dB, dC)
         torch.cuda.synchronize()
         check_csr(dC.cpu().numpy(), C64, absC)
+
+
+def _halves_csr(S, rng, M, K):
+    """Rows of mixed lengths (empty, short, a few long ones) with columns drawn
+    over all of K or, for some rows, from one half only; unsorted, repeats
+    allowed (the B-row halves keep each row's entry order within a half)."""
+    lens = np.where(rng.random(M) < 0.2, 0, rng.integers(1, 60, size=M))
+    long_rows = rng.random(M) < 0.02
+    lens[long_rows] = rng.integers(500, 4000, size=int(long_rows.sum()))
+    K0 = K // 2
+    cols = []
+    for r in range(M):
+        side = rng.random()
+        lo, hi = (0, K0) if side < 0.15 else ((K0, K) if side < 0.3 else (0, K))
+        cols.append(rng.integers(lo, hi, size=int(lens[r])))
+    row_ptr = np.zeros(M + 1, np.int32)
+    row_ptr[1:] = np.cumsum(lens)
+    col = np.concatenate(cols).astype(np.int32) if cols else np.zeros(0, np.int32)
+    return S.HostCSR(M, K, row_ptr, col, rng.uniform(-1, 1, col.size).astype(np.float32))
+
+
+@pytest.mark.parametrize("chunk", range(2))
+def test_khalf_random(S, O, torch, chunk):
+    # merge-path over B-row halves on random shapes that qualify (N % 4 == 0,
+    # K x N x 4 bytes over 4 MiB with half of the rows within it); a plan with
+    # a half under 512 entries is refused
+    rng = np.random.default_rng(7000 + chunk)
+    for case in range(10):
+        N = int(rng.choice([4, 8, 12, 16, 32, 64, 128, 192, 256]))
+        kmin, kmax = (1 << 20) // N + 1, (1 << 21) // N
+        K = int(rng.integers(kmin, kmax + 1))
+        M = int(rng.integers(1, 900))
+        A = _halves_csr(S, rng, M, K)
+        n0 = int((A.col_idx < K // 2).sum())
+        say(f"fuzz khalf chunk={chunk} case={case} M={M} K={K} N={N} nnz={A.nnz} half0={n0}")
+        if min(n0, A.nnz - n0) < 512:
+            with pytest.raises(S.SpmmError) as e:
+                S.KHalfPlan(A, N)
+            assert e.value.code == S.SPMM_UNSUPPORTED
+            continue
+        B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+        C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=8)
+        with S.KHalfPlan(A, N) as p:
+            dC = torch.full((M, N), float("nan"), device="cuda")
+            p.launch(torch.from_numpy(B).cuda(), dC)
+            torch.cuda.synchronize()
+            check_csr(dC.cpu().numpy(), C64, absC)

@@ -62,7 +62,9 @@ const char* backend_name(Backend b);
 // The CSR branch picks from the host CSR's row lengths: sub-wave row groups
 // (narrow B, short rows, N <= 128 on >= 4096 even rows), the merge-path
 // partition (a row of more than 2560 entries, its row table and carry
-// workspace set up once), or the row-block engine given the longest row.
+// workspace set up once; split over B-row halves, one per group of four XCDs,
+// when B is over one XCD's 4 MiB L2 and half of its rows fit), or the
+// row-block engine given the longest row.
 float spmm_hybrid_run(const HybridPlan& plan,
                       const CSR& h_A, const float* h_B, float* h_C,
                       int N, int warmup, int iters);

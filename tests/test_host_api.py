@@ -339,3 +339,30 @@ def test_khalf_runs(S):
                             list(range(5)), np.ones(100, np.float32))
     first, last = S.khalf_runs(A.row_ptr, A.nnz, S.nnz_split_rows(A, 10))
     assert first.tolist() == [-1, 1, -1] and last.tolist() == [-1, 9, -1]
+
+
+def test_khalf_runs_errors(S):
+    import ctypes
+    rp = np.array([0, 2, 4], np.int32)
+    rows = np.array([0, 2], np.int32)
+    first = np.empty(2, np.int32)
+    last = np.empty(2, np.int32)
+    L = S.lib()
+    # parts < 1, negative sizes, missing arrays
+    assert L.spmm_c_khalf_runs(S._ptr(rp), 2, 4, S._ptr(rows), 0, S._ptr(first),
+                               S._ptr(last)) == S.SPMM_INVALID
+    assert L.spmm_c_khalf_runs(S._ptr(rp), -1, 4, S._ptr(rows), 1, S._ptr(first),
+                               S._ptr(last)) == S.SPMM_INVALID
+    assert L.spmm_c_khalf_runs(None, 2, 4, S._ptr(rows), 1, S._ptr(first),
+                               S._ptr(last)) == S.SPMM_INVALID
+    assert L.spmm_c_khalf_runs(S._ptr(rp), 2, 4, None, 1, S._ptr(first),
+                               S._ptr(last)) == S.SPMM_INVALID
+    assert b"null" in L.spmm_c_last_error()
+    # one part: nothing continues
+    f, l = S.khalf_runs(rp, 4, rows)
+    assert f.tolist() == [-1, -1] and l.tolist() == [-1, -1]
+    # the plan entry points refuse null arguments without touching the GPU
+    assert L.spmm_c_khalf_plan_create(None, 128, ctypes.byref(ctypes.c_void_p())) == \
+        S.SPMM_INVALID
+    assert L.spmm_c_khalf_launch(None, None, None, None) == S.SPMM_INVALID
+    L.spmm_c_khalf_plan_destroy(None)

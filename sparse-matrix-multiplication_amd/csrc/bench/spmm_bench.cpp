@@ -69,9 +69,12 @@ void print_usage(const char* prog) {
                  "  --batch INT      launches per timed batch (default 50)\n"
                  "  --bin PATH       load CSR from binary file (overrides --m/--k/--density)\n"
                  "  --kernel STR     baseline | memopt | memopt_v2 | tiled | tiled_v2 | tiled_v3\n"
-                 "                   | tiled_v4 | csr_auto | wmma | hybrid | unified | both | all\n"
+                 "                   | tiled_v4 | csr_auto | split | khalf | wmma | hybrid | unified\n"
+                 "                   | both | all\n"
                  "                   both = baseline + memopt (default); all = every kernel;\n"
-                 "                   csr_auto = the CSR form the hybrid picks, timed in batches\n"
+                 "                   csr_auto = the CSR form the hybrid picks, timed in batches;\n"
+                 "                   split / khalf = the merge-path form / over B-row halves\n"
+                 "                   whatever the hybrid would pick\n"
                  "  --cpu-threads INT host threads of the fp64 reference (default: all)\n"
                  "  --cpu-reps INT   timed repetitions of the fp64 reference (default 3)\n"
                  "  --no-cpu-1t      skip the one-thread run of the fp64 reference\n"
@@ -235,13 +238,23 @@ int main(int argc, char** argv) {
         results.push_back(r);
     }
 
-    if (ks == "csr_auto" || ks == "all") {
+    if (ks == "csr_auto" || ks == "split" || ks == "khalf" || ks == "all") {
         // The CSR form spmm_hybrid_run's CSR branch picks from the row lengths
         // (row groups, the engine with the longest row as hint, the
         // merge-path partition, or merge-path over B-row halves), timed like
         // the kernels above.
         namespace eng = spmm::engine;
-        const eng::CsrChoice ch = eng::choose_csr_form(h_A, N);
+        eng::CsrChoice ch = eng::choose_csr_form(h_A, N);
+        if (ks == "split") {
+            if (h_A.nnz < 1) {
+                std::fprintf(stderr, "split: the matrix has no nonzeros\n");
+                std::exit(EXIT_FAILURE);
+            }
+            ch.form  = eng::CsrForm::Split;
+            ch.parts = eng::split_partition_parts(h_A.nnz);
+        } else if (ks == "khalf") {
+            ch.form = eng::CsrForm::KHalf;
+        }
         int* d_rows = nullptr;
         float* d_carry = nullptr;
         eng::SplitPlan plan;
@@ -249,7 +262,7 @@ int main(int argc, char** argv) {
         if (ch.form == eng::CsrForm::KHalf) {
             const eng::Error e = eng::khalf_plan_build(h_A, N, &khalf);
             if (e.status != eng::kOk) {
-                std::fprintf(stderr, "csr_auto plan failed: %s\n", e.message.c_str());
+                std::fprintf(stderr, "B-row halves plan failed: %s\n", e.message.c_str());
                 std::exit(EXIT_FAILURE);
             }
         }
@@ -276,7 +289,9 @@ int main(int argc, char** argv) {
             }
         };
         Result r;
-        r.name = std::string("csr_auto[") + eng::csr_form_name(ch.form) + "]";
+        r.name = ks == "split" || ks == "khalf"
+                     ? ks
+                     : std::string("csr_auto[") + eng::csr_form_name(ch.form) + "]";
         time_launches(launch, args, &r.time_ms, &r.single_ms);
         r.cold_ms = cold(launch);
         fetch_compare(r);

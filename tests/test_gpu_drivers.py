@@ -79,6 +79,25 @@ def test_bench_csr_auto(args, form):
     assert float(d["rel_l2_err"]) < 1e-6 and float(d["cold_ms"]) > 0
 
 
+@pytest.mark.parametrize("kernel", ["split", "khalf"])
+def test_bench_forced_merge_path_forms(kernel):
+    # the merge-path form and its B-row halves, whatever the hybrid would pick
+    r = _run([BENCH, "--m", "2048", "--k", "12288", "--n", "128", "--pattern", "power-law",
+              "--mean-deg", "200", "--cap", "4096", "--kernel", kernel, "--warmup", "1",
+              "--iters", "3", "--batch", "4", "--cpu-reps", "1", "--no-cpu-1t"])
+    assert r.returncode == 0, r.stderr
+    d = _lines(r.stdout, "kernel=")[0]
+    assert d["kernel"] == kernel and float(d["rel_l2_err"]) < 1e-6
+
+
+def test_bench_khalf_refused_on_small_b():
+    # B of 1 MiB fits one L2: the halves' plan refuses, the driver says so
+    r = _run([BENCH, "--m", "512", "--k", "2048", "--n", "128", "--pattern", "power-law",
+              "--mean-deg", "100", "--cap", "1500", "--kernel", "khalf", "--warmup", "1",
+              "--iters", "2", "--batch", "2", "--cpu-reps", "1", "--no-cpu-1t"])
+    assert r.returncode != 0 and "B-row halves plan failed" in r.stderr
+
+
 def test_bench_wmma_exact_on_fp16_inputs():
     r = _run([BENCH, "--m", "512", "--k", "512", "--n", "64", "--pattern", "block-diagonal",
               "--block", "64", "--fp16-values", "--kernel", "wmma", "--warmup", "1",

@@ -83,3 +83,34 @@ def test_empty_input_fails(tmp_path):
     p = tmp_path / "empty.log"
     p.write_text("nothing here\n")
     assert R.main([str(p)]) == 1
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                      "reference_roofline_rows.csv")
+
+
+def test_byte_model_matches_the_reference_roofline_rows():
+    # The reference's committed sweep (reports/data/sweep.csv, 108 rows over 9
+    # kernels and 4 sizes) beside two columns its roofline script derived from
+    # it (reports/data/roofline.csv, scripts/roofline.py:177-205): arithmetic
+    # intensity and effective bandwidth depend only on the CSR byte model and
+    # the measured time, not on the GPU.  A dropped row-pointer term, a 4-byte
+    # instead of 8-byte entry or a fp16 B would each miss by far more than the
+    # tolerance.
+    rows = R.parse_sweep_csv(GOLDEN)
+    with open(GOLDEN, newline="") as f:
+        ref = list(csv.DictReader(f))
+    assert len(rows) == len(ref) == 108
+    res = R.analyse(rows)
+    mfma = 0
+    for row, r, g in zip(rows, res, ref):
+        b = R.csr_bytes(row["m"], row["k"], row["n"], row["nnz"])
+        ai, eff = float(g["ai_flop_per_byte"]), float(g["eff_dram_bw_gbs"])
+        assert 2.0 * row["nnz"] * row["n"] / b == pytest.approx(ai, rel=1e-12)
+        assert b / (row["time_ms"] * 1.0e6) == pytest.approx(eff, rel=1e-12)
+        if R._is_mfma(row["kernel"]):
+            mfma += 1  # priced on BSR bytes here, on CSR bytes in the reference
+            continue
+        assert r["ai_flop_per_byte"] == pytest.approx(ai, rel=1e-12)
+        assert r["eff_hbm_gbs"] == pytest.approx(eff, rel=1e-12)
+    assert mfma == 12

@@ -17,8 +17,9 @@ steady; `warmup` reports the count), then K steps back to back on torch's
 current stream between two events on that stream, synchronised on both
 sides.  With an explicit --warmup W the contract figure uses exactly W; the
 steps then run well above their steady time (MI355X, --warmup 5 --steps 20:
-c2 18.9 against 17.1 us, c1 8.0 against 5.9, c5 64.5 against 59.7; a copy
-kernel run first does not shorten it, 2000 launches of the same step do), so
+c2 18.9 against 17.1 us, c1 8.0 against 5.9, c5 64.5 against 59.7; the
+shader clock is already at 2.4 GHz, a copy kernel run first does not shorten
+it, 2000 launches of the same step do), so
 each block also carries `steady`: the same step after at least 0.1 s of
 untimed launches, 500 timed, measured afterwards.  `cold_ms_median` is the median of
 single launches each preceded by a 512 MiB write that evicts L2 (4 MiB per

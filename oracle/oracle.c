@@ -225,6 +225,29 @@ void oracle_csr_spmm_f64(int M, int N, const int* row_ptr, const int* col_idx,
 }
 
 /* ======================================================================
+ * CSR SpMM as the reference's baseline kernel computes it
+ * (src/kernels/spmm_baseline.cu:11-25): per output, sum = 0.f, then
+ * sum += values[p] * B[col_idx[p]][j] for p in CSR order, which nvcc's default
+ * contraction makes one fused multiply-add per entry.  fmaf is the correctly
+ * rounded fused operation; this file is built with -ffp-contract=off, so no
+ * other expression is fused.
+ * ====================================================================== */
+
+void oracle_csr_spmm_f32_fma(int M, int N, const int* row_ptr, const int* col_idx,
+                             const float* values, const float* B, float* C) {
+    for (int r = 0; r < M; ++r) {
+        float* crow = C + (size_t)r * N;
+        for (int n = 0; n < N; ++n) {
+            float sum = 0.f;
+            for (int p = row_ptr[r]; p < row_ptr[r + 1]; ++p) {
+                sum = fmaf(values[p], B[(size_t)col_idx[p] * N + n], sum);
+            }
+            crow[n] = sum;
+        }
+    }
+}
+
+/* ======================================================================
  * fp16, round to nearest even (IEEE 754 binary16)
  * ==================================================================== */
 uint16_t oracle_f32_to_f16(float x) {

@@ -20,6 +20,9 @@
  *   coo_to_csr                 numpy lexsort on random triplets with duplicates
  *   csr_spmm_f64               scipy.sparse CSR @ dense in float64, identity,
  *                              empty rows, single entries, brute force
+ *   csr_spmm_f32_fma           an fp64 restatement of each fused step on random
+ *                              inputs, exact integer cases, and a case where the
+ *                              fused and the unfused chain round differently
  *   f32_to_f16 / f16_to_f32    numpy float16 conversion (RNE) over edge cases
  *   bsr_build / bsr_stats      brute-force densification, known block counts and
  *                              fill-in from reports/tensor_core_wmma.md:43-56,
@@ -77,6 +80,12 @@ int oracle_coo_to_csr(int rows, long n, const int* r, const int* c, const float*
 void oracle_csr_spmm_f64(int M, int N, const int* row_ptr, const int* col_idx,
                          const float* values, const float* B, double* C, double* abs_c,
                          int threads);
+
+/* ---- CSR SpMM, fp32 fused chain (spmm_baseline.cu:11-25) --------------
+ * C[r][j] = fmaf(values[p], B[col_idx[p]][j], ...) from 0.f in CSR order: the
+ * reference's baseline kernel bit for bit (nvcc contracts its a*b + sum). */
+void oracle_csr_spmm_f32_fma(int M, int N, const int* row_ptr, const int* col_idx,
+                             const float* values, const float* B, float* C);
 
 /* ---- fp16 ------------------------------------------------------------ */
 /* __float2half round-to-nearest-even (bsr.cu:94-96, spmm_wmma.cu:22) */

@@ -27,6 +27,7 @@ _SIGS = {
     "oracle_generate_dense": (None, [_int, _int, _int, _vp]),
     "oracle_coo_to_csr": (_int, [_int, _long, _vp, _vp, _vp, _vp, _vp, _vp]),
     "oracle_csr_spmm_f64": (None, [_int, _int, _vp, _vp, _vp, _vp, _vp, _vp, _int]),
+    "oracle_csr_spmm_f32_fma": (None, [_int, _int, _vp, _vp, _vp, _vp, _vp]),
     "oracle_f32_to_f16": (ctypes.c_uint16, [_float]),
     "oracle_f16_to_f32": (_float, [ctypes.c_uint16]),
     "oracle_f32_to_f16_array": (None, [_vp, _vp, _long]),
@@ -122,6 +123,19 @@ def csr_spmm_f64(row_ptr, col_idx, values, B, threads: int = 1, with_abs: bool =
     lib().oracle_csr_spmm_f64(M, N, _p(row_ptr), _p(col_idx), _p(values), _p(B), _p(C),
                               _p(A) if A is not None else 0, threads)
     return C, A
+
+
+def csr_spmm_f32_fma(row_ptr, col_idx, values, B):
+    """The reference baseline kernel's fp32 fused chain (spmm_baseline.cu:11-25)."""
+    row_ptr = np.ascontiguousarray(row_ptr, np.int32)
+    col_idx = np.ascontiguousarray(col_idx, np.int32)
+    values = np.ascontiguousarray(values, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    M = row_ptr.size - 1
+    N = B.shape[1]
+    C = np.empty((M, N), np.float32)
+    lib().oracle_csr_spmm_f32_fma(M, N, _p(row_ptr), _p(col_idx), _p(values), _p(B), _p(C))
+    return C
 
 
 def f32_to_f16(x: np.ndarray) -> np.ndarray:

@@ -138,6 +138,54 @@ def test_csr_spmm_special_cases(O):
     assert np.array_equal(C[3], 0.75 * Bd[2])  # both scalings are exact in fp64
 
 
+def _fused_chain_f64(rp, ci, va, B):
+    # Each step sum = fma(v, b, sum) restated in fp64: the product of two fp32
+    # values is exact in fp64, the sum rounds once to fp64 and once to fp32
+    # (equal to the single fused rounding unless the fp64 sum lands on an fp32
+    # rounding midpoint, which these inputs never do).
+    M, N = rp.size - 1, B.shape[1]
+    C = np.zeros((M, N), np.float32)
+    Bd = B.astype(np.float64)
+    for r in range(M):
+        s = np.zeros(N, np.float32)
+        for p in range(rp[r], rp[r + 1]):
+            s = (np.float64(va[p]) * Bd[ci[p]] + s.astype(np.float64)).astype(np.float32)
+        C[r] = s
+    return C
+
+
+def test_csr_spmm_f32_fma_matches_a_step_restatement(O):
+    rp, ci, va = O.uniform_csr(120, 90, 0.08, 21)
+    B = O.dense(90, 13, 22)
+    C = O.csr_spmm_f32_fma(rp, ci, va, B)
+    assert np.array_equal(C.view(np.uint32), _fused_chain_f64(rp, ci, va, B).view(np.uint32))
+
+
+def test_csr_spmm_f32_fma_exact_and_fused(O):
+    # small integers: every product and partial sum is exact, so the chain is
+    # the exact product
+    rng = np.random.default_rng(5)
+    rp = np.array([0, 3, 3, 7], np.int32)
+    ci = rng.integers(0, 6, 7).astype(np.int32)
+    va = rng.integers(-8, 9, 7).astype(np.float32)
+    B = rng.integers(-50, 51, (6, 4)).astype(np.float32)
+    C = O.csr_spmm_f32_fma(rp, ci, va, B)
+    C64, _ = O.csr_spmm_f64(rp, ci, va, B)
+    assert np.array_equal(C.astype(np.float64), C64) and np.all(C[1] == 0)
+    # one fused step differs from multiply-then-add: after sum = -1, the
+    # product (1 + 2^-12)^2 = 1 + 2^-11 + 2^-24 is exact inside the fused
+    # operation (sum 2^-11 + 2^-24), while rounding it to fp32 first ties to
+    # even at 1 + 2^-11 (sum 2^-11)
+    x = np.float32(1 + 2.0 ** -12)
+    rp = np.array([0, 2], np.int32)
+    ci = np.array([0, 1], np.int32)
+    va = np.array([1.0, x], np.float32)
+    B = np.array([[-1.0], [x]], np.float32)
+    C = O.csr_spmm_f32_fma(rp, ci, va, B)
+    assert C[0, 0] == np.float32(2.0 ** -11 + 2.0 ** -24)
+    assert np.float32(np.float32(x * x) + np.float32(-1.0)) == np.float32(2.0 ** -11)
+
+
 def test_fp16_rne_matches_numpy(O):
     rng = np.random.default_rng(5)
     special = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, 1e6, -1e6,

@@ -118,17 +118,21 @@ def test_configs(S, torch, config_refs, kernel, cfg):
     say(f"  rel_l2={rel:.3e}")
 
 
-def test_baseline_is_the_reference_chain_bit_for_bit(S, O, torch, edge_cases, config_refs):
-    # spmm_baseline (spmm_baseline.cu:11-25) is sum += value * b from 0.f in
-    # CSR order, one fused multiply-add per entry under nvcc's default
-    # contraction. The lane-per-output kernel computes the same chain, so its
-    # results equal the CPU restatement of it bit for bit.
+@pytest.mark.parametrize("kernel", ["baseline", "memopt", "memopt_v2"])
+def test_sequential_roles_are_the_reference_chain_bit_for_bit(S, O, torch, edge_cases,
+                                                               config_refs, kernel):
+    # spmm_baseline, spmm_memopt and spmm_memopt_v2 (spmm_baseline.cu:11-25,
+    # spmm_memopt.cu:17-37, spmm_memopt_v2.cu) each compute an output as
+    # sum += value * b from 0.f in CSR order, one fused multiply-add per entry
+    # under nvcc's default contraction; they differ only in how threads map to
+    # outputs. The lane-per-output and wave-per-row kernels compute the same
+    # chain, so their results equal the CPU restatement bit for bit.
     cases = [(name, A, B) for name, (A, B, _, _) in edge_cases.items()]
     A, B, _, _ = config_refs("c1")
     cases.append(("c1", A, B))
     for name, A, B in cases:
-        say(f"csr baseline bitwise case={name} M={A.num_rows} N={B.shape[1]} nnz={A.nnz}")
-        C = _run(S, torch, "baseline", A, B)
+        say(f"csr {kernel} bitwise case={name} M={A.num_rows} N={B.shape[1]} nnz={A.nnz}")
+        C = _run(S, torch, kernel, A, B)
         ref = O.csr_spmm_f32_fma(A.row_ptr, A.col_idx, A.values, B)
         assert np.array_equal(C.view(np.uint32), ref.view(np.uint32)), name
 

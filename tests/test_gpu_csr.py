@@ -137,6 +137,27 @@ def test_sequential_roles_are_the_reference_chain_bit_for_bit(S, O, torch, edge_
         assert np.array_equal(C.view(np.uint32), ref.view(np.uint32)), name
 
 
+@pytest.mark.parametrize("cfg", ["c1", "c2"])
+def test_row_groups_one_entry_lane_is_the_reference_chain(S, O, torch, config_refs, cfg):
+    # The tiled roles' fast forms associate a row's sum differently from the
+    # reference's fused chain. The row groups with one entry lane per row do
+    # not: each lane sums its columns over the row's entries in CSR order
+    # with fused multiply-adds, so the option reproduces the reference kernels
+    # bit for bit (for rows that stay in their group, as all of c1's and c2's do).
+    A, B, _, _ = config_refs(cfg)
+    opts = S.EngineOptsT()
+    opts.row_groups = 1
+    opts.entry_lanes = 1
+    say(f"csr row groups, one entry lane, bitwise config={cfg}")
+    dA = S.DeviceCSR(A)
+    dB = torch.from_numpy(B).cuda()
+    dC = torch.full((A.num_rows, B.shape[1]), float("nan"), dtype=torch.float32, device="cuda")
+    S.launch_repeat_opts(dA, dB, dC, opts, 1)
+    torch.cuda.synchronize()
+    ref = O.csr_spmm_f32_fma(A.row_ptr, A.col_idx, A.values, B)
+    assert np.array_equal(dC.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("cfg", ["c3", "c4"])
 def test_engine_on_fp16_configs(S, torch, config_refs, cfg):
     # the CSR back end must also be right on the structured configs: the

@@ -148,6 +148,7 @@ def test_row_groups_one_entry_lane_is_the_reference_chain(S, O, torch, config_re
     opts = S.EngineOptsT()
     opts.row_groups = 1
     opts.entry_lanes = 1
+    opts.unroll = 4  # four entries in flight per lane (same order, faster)
     say(f"csr row groups, one entry lane, bitwise config={cfg}")
     dA = S.DeviceCSR(A)
     dB = torch.from_numpy(B).cuda()

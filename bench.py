@@ -147,9 +147,24 @@ def build_pattern(S, torch, name: str):
         hb = S.bsr_from_csr_host(A)
         dA = S.DeviceBSR(hb)
         B16 = S.float_to_half(torch.from_numpy(B).cuda())
-        P.update(host_bsr=hb, blocks=hb.num_blocks, form="wmma", dtype="f16 in, f32 accumulate")
-        P["launch"] = lambda reps: S.launch_repeat("wmma", dA, B16, C, reps, cur())
-        P["keep"] = (dA, B16)
+        P.update(host_bsr=hb, blocks=hb.num_blocks, dtype="f16 in, f32 accumulate")
+        # spmm_hybrid_run's MFMA branch: the run-panel kernel when the block
+        # structure is runs (its plan built with the BSR, outside the steps),
+        # else the record kernel.
+        try:
+            tp = S.BsrTilePlan(dA)
+        except S.SpmmError as e:
+            if e.code != S.SPMM_UNSUPPORTED:
+                raise
+            tp = None
+        if tp is not None:
+            P["form"] = "tile"
+            P["launch"] = lambda reps: tp.launch_repeat(B16, C, reps, stream=cur())
+            P["keep"] = (dA, B16, tp)
+        else:
+            P["form"] = "wmma"
+            P["launch"] = lambda reps: S.launch_repeat("wmma", dA, B16, C, reps, cur())
+            P["keep"] = (dA, B16)
         return P
     form, opts, parts = S.csr_auto_form(A, N)
     dB = torch.from_numpy(B).cuda()

@@ -279,6 +279,42 @@ int spmm_c_wmma(const spmm_bsr_t* d_bsr, const uint16_t* d_B_fp16, float* d_C, i
 int spmm_c_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B_fp16, float* d_C, int N,
                      const spmm_bsr_opts_t* opts, void* stream);
 
+/* Run-panel form of spmm_wmma (no counterpart in the reference; the form
+ * spmm_c_hybrid_run runs when every block-row of the BSR is a run of
+ * consecutive block-columns and each panel's runs cover their union without a
+ * gap, as in banded and block-diagonal matrices).  The plan holds one record
+ * per panel of rows_per_panel (4 or 8) block-rows; the kernel then reads no
+ * row_ptr / col_idx.
+ * create: reads the device BSR's row_ptr and col_idx back (synchronises
+ *   `stream`) and uploads the records; SPMM_UNSUPPORTED when the structure is
+ *   not runs as above (use spmm_c_wmma then).
+ * launch: d_B (num_cols x N fp16 bits) and d_C (num_rows x N fp32) 16-byte
+ *   aligned, N % 8 == 0, N * 2 <= 16383; shape < 0 picks the default kernel
+ *   shape (spmm_c_bsr_tile_shape lists them); the result equals spmm_c_wmma's
+ *   within fp32 rounding (same products, same pairwise K order).
+ * records: the host part of create, for callers with a host copy of the
+ *   block structure: panels x 32 ints into records_out (room for
+ *   ceil(block_rows / rows_per_panel) x 32), *max_union_out the widest union. */
+typedef struct spmm_bsr_tile_plan spmm_bsr_tile_plan_t;
+int  spmm_c_bsr_tile_plan_create(const spmm_bsr_t* d_A, int rows_per_panel, void* stream,
+                                 spmm_bsr_tile_plan_t** plan_out);
+int  spmm_c_bsr_tile_launch(const spmm_bsr_tile_plan_t* plan, const spmm_bsr_t* d_A,
+                            const uint16_t* d_B_fp16, float* d_C, int N, int shape,
+                            void* stream);
+void spmm_c_bsr_tile_plan_destroy(spmm_bsr_tile_plan_t* plan);
+int  spmm_c_bsr_tile_plan_info(const spmm_bsr_tile_plan_t* plan, int* panels_out,
+                               int* rows_per_panel_out, int* max_union_out);
+int  spmm_c_bsr_tile_records(const int* row_ptr, const int* col_idx, int block_rows,
+                             int block_cols, int rows_per_panel, int* records_out,
+                             int* max_union_out);
+/* Kernel shapes: count, and shape id's (rows per panel, columns per
+ * workgroup, wave columns, slots per chunk, chunk buffers, kind: 0 ring with
+ * A in VGPRs, 1 whole union with A in VGPRs, 2 producer / consumer waves);
+ * the default shape for a plan and N columns. */
+int  spmm_c_bsr_tile_shape_count(void);
+int  spmm_c_bsr_tile_shape(int id, int* fields_out /* 6 ints */);
+int  spmm_c_bsr_tile_default_shape(const spmm_bsr_tile_plan_t* plan, int N);
+
 /* ---- hybrid dispatch (spmm_hybrid.h:48-64) ---------------------------- */
 /* The wide-B cut-off (N >= 256) and the per-N MI355X crossover; no
  * counterpart in the reference (its default is the constant 2.0). */
@@ -319,6 +355,9 @@ int spmm_c_launch_repeat_khalf(const spmm_khalf_plan_t* plan, const float* d_B, 
 int spmm_c_launch_repeat_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B_fp16,
                                    float* d_C, int N, const spmm_bsr_opts_t* opts, int reps,
                                    void* stream);
+int spmm_c_launch_repeat_bsr_tile(const spmm_bsr_tile_plan_t* plan, const spmm_bsr_t* d_A,
+                                  const uint16_t* d_B_fp16, float* d_C, int N, int shape,
+                                  int reps, void* stream);
 /* Times `reps` back-to-back launches between two hipEvents recorded on
  * `stream`; writes the elapsed milliseconds of the whole batch. */
 int spmm_c_time_repeat(int kernel_id, const void* d_A_any, const void* d_B, float* d_C,

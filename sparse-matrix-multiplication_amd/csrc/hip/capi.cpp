@@ -667,6 +667,104 @@ int spmm_c_khalf_runs(const int* row_ptr, int M, long long nnz, const int* split
     return ok();
 }
 
+struct spmm_bsr_tile_plan {
+    spmm::engine::BsrTilePlan p;
+};
+
+int spmm_c_bsr_tile_plan_create(const spmm_bsr_t* d_A, int rows_per_panel, void* stream,
+                                spmm_bsr_tile_plan_t** plan_out) {
+    if (d_A == nullptr || plan_out == nullptr) return set_error(SPMM_INVALID, "null argument");
+    *plan_out = nullptr;
+    spmm_bsr_tile_plan_t* plan = new (std::nothrow) spmm_bsr_tile_plan_t;
+    if (plan == nullptr) return set_error(SPMM_NO_MEMORY, "host allocation failed");
+    const int rc = guarded([&] {
+        return from_engine(spmm::engine::bsr_tile_plan_build(to_cpp(*d_A), rows_per_panel,
+                                                             &plan->p, as_stream(stream)));
+    });
+    if (rc != SPMM_OK) {
+        spmm::engine::bsr_tile_plan_free(&plan->p);
+        delete plan;
+        return rc;
+    }
+    *plan_out = plan;
+    return ok();
+}
+
+int spmm_c_bsr_tile_launch(const spmm_bsr_tile_plan_t* plan, const spmm_bsr_t* d_A,
+                           const uint16_t* d_B_fp16, float* d_C, int N, int shape,
+                           void* stream) {
+    if (plan == nullptr || d_A == nullptr) return set_error(SPMM_INVALID, "null argument");
+    return from_engine(spmm::engine::launch_bsr_tile(plan->p, to_cpp(*d_A),
+                                                     reinterpret_cast<const half*>(d_B_fp16),
+                                                     d_C, N, as_stream(stream), shape));
+}
+
+void spmm_c_bsr_tile_plan_destroy(spmm_bsr_tile_plan_t* plan) {
+    if (plan == nullptr) return;
+    spmm::engine::bsr_tile_plan_free(&plan->p);
+    delete plan;
+}
+
+int spmm_c_bsr_tile_plan_info(const spmm_bsr_tile_plan_t* plan, int* panels_out,
+                              int* rows_per_panel_out, int* max_union_out) {
+    if (plan == nullptr) return set_error(SPMM_INVALID, "null plan");
+    if (panels_out) *panels_out = plan->p.panels;
+    if (rows_per_panel_out) *rows_per_panel_out = plan->p.R;
+    if (max_union_out) *max_union_out = plan->p.max_union;
+    return ok();
+}
+
+int spmm_c_bsr_tile_records(const int* row_ptr, const int* col_idx, int block_rows,
+                            int block_cols, int rows_per_panel, int* records_out,
+                            int* max_union_out) {
+    if (row_ptr == nullptr || records_out == nullptr || max_union_out == nullptr ||
+        (block_rows > 0 && row_ptr[block_rows] > 0 && col_idx == nullptr)) {
+        return set_error(SPMM_INVALID, "null argument");
+    }
+    return guarded([&] {
+        std::vector<int> desc;
+        int mu = 0;
+        const int rc = from_engine(spmm::engine::bsr_tile_plan_from_host(
+            row_ptr, col_idx, block_rows, block_cols, rows_per_panel, &desc, &mu));
+        if (rc != SPMM_OK) return rc;
+        std::copy(desc.begin(), desc.end(), records_out);
+        *max_union_out = mu;
+        return ok();
+    });
+}
+
+int spmm_c_bsr_tile_shape_count(void) { return spmm::engine::tile_shape_count(); }
+
+int spmm_c_bsr_tile_shape(int id, int* fields_out) {
+    if (fields_out == nullptr) return set_error(SPMM_INVALID, "null argument");
+    if (id < 0 || id >= spmm::engine::tile_shape_count()) {
+        return set_error(SPMM_INVALID, "unknown tile shape");
+    }
+    const spmm::engine::TileShape& t = spmm::engine::kTileShapes[id];
+    const int f[6] = {t.R, t.NT, t.WC, t.CS, t.NB, t.KIND};
+    std::copy(f, f + 6, fields_out);
+    return ok();
+}
+
+int spmm_c_bsr_tile_default_shape(const spmm_bsr_tile_plan_t* plan, int N) {
+    if (plan == nullptr) return set_error(SPMM_INVALID, "null plan");
+    return spmm::engine::default_tile_shape(plan->p.R, plan->p.max_union, plan->p.num_rows, N);
+}
+
+int spmm_c_launch_repeat_bsr_tile(const spmm_bsr_tile_plan_t* plan, const spmm_bsr_t* d_A,
+                                  const uint16_t* d_B_fp16, float* d_C, int N, int shape,
+                                  int reps, void* stream) {
+    if (plan == nullptr || d_A == nullptr) return set_error(SPMM_INVALID, "null argument");
+    const spmm::BSR A = to_cpp(*d_A);
+    for (int i = 0; i < reps; ++i) {
+        const int rc = from_engine(spmm::engine::launch_bsr_tile(
+            plan->p, A, reinterpret_cast<const half*>(d_B_fp16), d_C, N, as_stream(stream),
+            shape));
+        if (rc != SPMM_OK) return rc;
+    }
+    return ok();
+}
+
 int spmm_c_tiled_v3_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, int N,
                          const spmm_engine_opts_t* opts, void* stream) {
     if (d_A == nullptr) return set_error(SPMM_INVALID, "null argument");

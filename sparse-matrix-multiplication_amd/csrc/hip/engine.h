@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <string>
+#include <vector>
 
 #include "spmm/bsr.h"
 #include "spmm/csr.h"
@@ -95,6 +96,67 @@ struct BsrOpts {
 
 Error launch_bsr(const BSR& d_A, const half* d_B, float* d_C, int N, hipStream_t stream,
                  const BsrOpts* opts = nullptr);
+
+// Run-panel plan of a BSR whose block-rows are runs of consecutive
+// block-columns (bsr_tile.hip).  Panel p = block-rows [pR, pR + R); its
+// record of kTileDescInts ints holds the union of the runs (first
+// block-column, width) and per block-row the run as union slots [lo, hi) and
+// the A block of slot lo.  Device memory is owned by the plan.
+constexpr int kTileDescInts = 32;
+struct BsrTilePlan {
+    int* desc       = nullptr;  // device, panels x kTileDescInts
+    int  R          = 0;        // block-rows per panel, 4 or 8
+    int  panels     = 0;
+    int  num_rows   = 0;        // the matrix the plan describes (checked at launch)
+    int  num_cols   = 0;
+    int  block_rows = 0;
+    int  num_blocks = 0;
+    int  max_union  = 0;        // widest panel union, in block-columns
+};
+// Kernel shapes (id, R, NT columns per workgroup, WC wave columns, CS slots
+// per staged chunk, NB chunk buffers, KIND).  KIND 0: A operands in VGPRs, a
+// ring of NB B buffers with NB - 1 chunks in flight (any union width); 1: A
+// in VGPRs, the whole union in flight (widest union <= NB * CS); 2: producer
+// and consumer waves, A and B staged in LDS, the whole union in flight.
+struct TileShape {
+    int R, NT, WC, CS, NB, KIND;
+};
+#define SPMM_TILE_SHAPES(X)      \
+    X(0, 8, 64, 1, 4, 4, 2)      \
+    X(1, 4, 64, 1, 4, 3, 2)      \
+    X(2, 4, 128, 2, 4, 4, 2)     \
+    X(3, 4, 64, 1, 4, 4, 2)      \
+    X(4, 4, 128, 1, 4, 4, 2)     \
+    X(5, 4, 32, 1, 4, 3, 2)      \
+    X(6, 8, 64, 1, 4, 3, 2)      \
+    X(7, 4, 64, 1, 4, 4, 1)      \
+    X(8, 4, 32, 1, 4, 3, 1)      \
+    X(9, 4, 128, 2, 4, 5, 0)     \
+    X(10, 4, 64, 1, 4, 4, 0)     \
+    X(11, 8, 64, 1, 4, 5, 0)     \
+    X(12, 4, 32, 1, 4, 4, 2)
+#define SPMM_TILE_ENTRY(ID, R_, NT_, WC_, CS_, NB_, KIND_) TileShape{R_, NT_, WC_, CS_, NB_, KIND_},
+constexpr TileShape kTileShapes[] = {SPMM_TILE_SHAPES(SPMM_TILE_ENTRY)};
+#undef SPMM_TILE_ENTRY
+int tile_shape_count();
+// The shape the hybrid and the C ABI use when none is given, for an M-row
+// matrix times N columns and a plan of R block-rows per panel whose widest
+// union is max_union block-columns.
+int default_tile_shape(int R, int max_union, int M, int N);
+// Block-rows per panel of the default shape for M rows and N columns.
+int default_tile_rows(int M, int N);
+// Host part of the plan build: the records, or kUnsupported when a block-row
+// is not a run or a panel's runs leave a gap.
+Error bsr_tile_plan_from_host(const int* row_ptr, const int* col_idx, int block_rows,
+                              int block_cols, int R, std::vector<int>* desc, int* max_union);
+// Reads the device BSR's row_ptr and col_idx back (synchronises `stream`) and
+// uploads the records.
+Error bsr_tile_plan_build(const BSR& d_A, int R, BsrTilePlan* out, hipStream_t stream);
+void  bsr_tile_plan_free(BsrTilePlan* p);
+// shape < 0: default_tile_shape.  kUnsupported unless N % 8 == 0, B, C and
+// the values are 16-byte aligned and the operands fit the buffer records.
+Error launch_bsr_tile(const BsrTilePlan& plan, const BSR& d_A, const half* d_B, float* d_C,
+                      int N, hipStream_t stream, int shape = -1);
 
 // CSR -> BSR on the device: allocates the BSR's three arrays (release with
 // bsr_free_device) and fills them exactly as bsr_from_csr_host would.  The

@@ -197,8 +197,36 @@ Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float
         SPMM_TRY_HIP(hipMalloc(&d_B16.p, sizeof(half) * (b_elems > 0 ? b_elems : 1)), "hipMalloc");
         SPMM_TRY(launch_float_to_half(d_B.as<float>(), d_B16.as<half>(),
                                       static_cast<long>(b_elems), nullptr));
+        // Structured matrices (every block-row a run of consecutive
+        // block-columns, each panel's runs covering their union) take the
+        // run-panel kernel; its plan is built here with the BSR, outside the
+        // timed launches, as the BSR itself is (spmm_hybrid.cu:78-85).  Other
+        // matrices take the record kernel, which needs only the BSR.
+        struct TileGuard {
+            BsrTilePlan p;
+            ~TileGuard() { bsr_tile_plan_free(&p); }
+        } tile;
+        bool tiled = false;
+        const Error planned =
+            bsr_tile_plan_build(bsr.view, default_tile_rows(M, N), &tile.p, nullptr);
+        if (planned.status == kOk) {
+            const Error first =
+                launch_bsr_tile(tile.p, bsr.view, d_B16.as<half>(), d_C.as<float>(), N, nullptr);
+            if (first.status == kOk) {
+                tiled = true;
+            } else if (first.status != kUnsupported) {
+                return first;
+            }
+        } else if (planned.status != kUnsupported) {
+            return planned;
+        }
         SPMM_TRY(time_median_launch(
-            [&] { return launch_bsr(bsr.view, d_B16.as<half>(), d_C.as<float>(), N, nullptr); },
+            [&] {
+                return tiled ? launch_bsr_tile(tile.p, bsr.view, d_B16.as<half>(), d_C.as<float>(),
+                                               N, nullptr)
+                             : launch_bsr(bsr.view, d_B16.as<half>(), d_C.as<float>(), N,
+                                          nullptr);
+            },
             warmup, iters, ms));
     } else {
         // The reference launches spmm_tiled_v3 over all rows

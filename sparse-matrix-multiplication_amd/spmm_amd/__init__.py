@@ -142,6 +142,16 @@ _SIGNATURES = {
     "spmm_c_wmma": (_int, [_P(BsrT), _vp, _vp, _int, _vp]),
     "spmm_c_wmma_opts": (_int, [_P(BsrT), _vp, _vp, _int, _P(BsrOptsT), _vp]),
     "spmm_c_launch_repeat_wmma_opts": (_int, [_P(BsrT), _vp, _vp, _int, _P(BsrOptsT), _int, _vp]),
+    "spmm_c_bsr_tile_plan_create": (_int, [_P(BsrT), _int, _vp, _P(_vp)]),
+    "spmm_c_bsr_tile_launch": (_int, [_vp, _P(BsrT), _vp, _vp, _int, _int, _vp]),
+    "spmm_c_bsr_tile_plan_destroy": (None, [_vp]),
+    "spmm_c_bsr_tile_plan_info": (_int, [_vp, _P(ctypes.c_int), _P(ctypes.c_int),
+                                         _P(ctypes.c_int)]),
+    "spmm_c_bsr_tile_records": (_int, [_vp, _vp, _int, _int, _int, _vp, _P(ctypes.c_int)]),
+    "spmm_c_bsr_tile_shape_count": (_int, []),
+    "spmm_c_bsr_tile_shape": (_int, [_int, _vp]),
+    "spmm_c_bsr_tile_default_shape": (_int, [_vp, _int]),
+    "spmm_c_launch_repeat_bsr_tile": (_int, [_vp, _P(BsrT), _vp, _vp, _int, _int, _int, _vp]),
     "spmm_c_hybrid_default_threshold": (_float, []),
     "spmm_c_hybrid_default_threshold_for": (_float, [ctypes.c_int]),
     "spmm_c_hybrid_choose": (_int, [_P(CsrT), _int, _float, _P(HybridPlanT)]),
@@ -782,6 +792,98 @@ class KHalfPlan:
     def close(self) -> None:
         if getattr(self, "_h", None) is not None:
             lib().spmm_c_khalf_plan_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+TILE_SHAPE_FIELDS = ("R", "NT", "WC", "CS", "NB", "KIND")
+
+
+def bsr_tile_shapes():
+    """The run-panel kernel's shapes: a list of dicts with TILE_SHAPE_FIELDS."""
+    out = []
+    for i in range(lib().spmm_c_bsr_tile_shape_count()):
+        f = np.zeros(6, np.int32)
+        _check(lib().spmm_c_bsr_tile_shape(i, _ptr(f)))
+        out.append(dict(zip(TILE_SHAPE_FIELDS, (int(x) for x in f))))
+    return out
+
+
+def bsr_tile_records(row_ptr, col_idx, block_cols: int, rows_per_panel: int = 4):
+    """Host part of the run-panel plan: (records (panels x 32 int32), widest
+    union).  Raises SpmmError(SPMM_UNSUPPORTED) unless every block-row is a
+    run of consecutive block-columns and each panel's runs cover their union."""
+    rp = np.ascontiguousarray(row_ptr, np.int32)
+    ci = np.ascontiguousarray(col_idx, np.int32)
+    block_rows = rp.size - 1
+    panels = (block_rows + rows_per_panel - 1) // rows_per_panel
+    rec = np.zeros((max(panels, 1), 32), np.int32)
+    mu = ctypes.c_int()
+    _check(lib().spmm_c_bsr_tile_records(_ptr(rp), _ptr(ci) if ci.size else 0, block_rows,
+                                         int(block_cols), int(rows_per_panel), _ptr(rec),
+                                         ctypes.byref(mu)))
+    return rec[:panels], mu.value
+
+
+class BsrTilePlan:
+    """Run-panel plan of a device BSR (no counterpart in the reference; the
+    form of spmm_wmma that spmm_hybrid_run runs on structured matrices).  One
+    record per panel of rows_per_panel block-rows; creation reads the BSR's
+    block structure back from the device.  Raises SpmmError(SPMM_UNSUPPORTED)
+    when the structure is not runs (use launch_repeat("wmma", ...) then)."""
+
+    def __init__(self, A, rows_per_panel: int = 4, stream=None):
+        _torch()
+        self.A = A
+        self.num_rows, self.num_cols = A.num_rows, A.num_cols
+        self._h = None
+        handle = ctypes.c_void_p()
+        s = A.struct()
+        _check(lib().spmm_c_bsr_tile_plan_create(ctypes.byref(s), int(rows_per_panel),
+                                                 _stream_handle(stream), ctypes.byref(handle)))
+        self._h = handle
+        panels, rpp, mu = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        _check(lib().spmm_c_bsr_tile_plan_info(self._h, ctypes.byref(panels), ctypes.byref(rpp),
+                                               ctypes.byref(mu)))
+        self.panels, self.rows_per_panel, self.max_union = panels.value, rpp.value, mu.value
+
+    def default_shape(self, N: int) -> int:
+        return int(lib().spmm_c_bsr_tile_default_shape(self._h, int(N)))
+
+    def _operands(self, B16, C):
+        if self._h is None:
+            raise SpmmError(SPMM_INVALID, "plan is closed")
+        return _csr_operands(self.A, B16, C, fp16=True)
+
+    def launch(self, B16, C=None, shape: int = -1, stream=None):
+        N, C = self._operands(B16, C)
+        s = self.A.struct()
+        _check(lib().spmm_c_bsr_tile_launch(self._h, ctypes.byref(s), B16.data_ptr(),
+                                            C.data_ptr(), N, int(shape), _stream_handle(stream)))
+        return C
+
+    def launch_repeat(self, B16, C, reps: int, shape: int = -1, stream=None) -> None:
+        """reps back-to-back launches (measurement helper)."""
+        N, C = self._operands(B16, C)
+        s = self.A.struct()
+        _check(lib().spmm_c_launch_repeat_bsr_tile(self._h, ctypes.byref(s), B16.data_ptr(),
+                                                   C.data_ptr(), N, int(shape), int(reps),
+                                                   _stream_handle(stream)))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None:
+            lib().spmm_c_bsr_tile_plan_destroy(self._h)
             self._h = None
 
     def __enter__(self):

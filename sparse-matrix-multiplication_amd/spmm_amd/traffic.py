@@ -33,7 +33,7 @@ COPY_BYTES = 256 * 1024 * 1024
 # Source files whose text decides what a pattern's launch runs, per backend.
 SOURCES = {
     "csr": ("csr_kernels.hip", "hybrid.cpp", "khalf.cpp"),
-    "wmma": ("bsr_kernels.hip",),
+    "wmma": ("bsr_kernels.hip", "bsr_tile.hip", "amdgcn.h"),
 }
 
 

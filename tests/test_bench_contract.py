@@ -26,8 +26,8 @@ def test_more_than_one_gpu_is_refused():
 
 def test_committed_traffic_matches_current_sources():
     # every pattern's capture is current: same source hash, same form
-    forms = {"c1": ("csr", "rowgroups"), "c2": ("csr", "engine"), "c3": ("wmma", "wmma"),
-             "c4": ("wmma", "wmma"), "c5": ("csr", "khalf")}
+    forms = {"c1": ("csr", "rowgroups"), "c2": ("csr", "engine"), "c3": ("wmma", "tile"),
+             "c4": ("wmma", "tile"), "c5": ("csr", "khalf")}
     for name, (backend, form) in forms.items():
         value, note = bench.load_traffic(name, backend, form)
         assert value is not None, f"{name}: {note}"

@@ -59,6 +59,7 @@ CASES = [
     ("diag", 1000, 1000, 40, 24),    # diagonal blocks straddling block-rows
     ("diag", 400, 400, 48, 320),     # wide N
     ("diag", 1024, 1024, 512, 32),   # unions of 32 block-columns: the ring only
+    ("diag", 1000, 1000, 128, 72),   # a partial last panel
 ]
 
 

@@ -126,8 +126,17 @@ typedef struct spmm_bsr_opts_t {
                        panel kernel: 16-column tiles per workgroup, 4 or 8 */
     int per_wave;   /* 1: wave kernel whatever row_group says */
     int depth;      /* wave kernel: block pairs in flight per wave, 1, 2, 4;
-                       panel kernel: LDS stages in flight, 2 or 4 */
+                       panel kernel: LDS stages in flight, 2 or 4.
+                       tiles / depth 0: the kernel's default.  Values no
+                       kernel has, or (row_group 1 / 4 / 8, per_wave) values
+                       the named kernel lacks, are SPMM_INVALID; under the
+                       automatic choice the chosen kernel's default replaces
+                       a value it lacks. */
     int xcd_order;  /* 0, 1 XCD-grouped workgroup order; 2 dispatch order */
+    int reserved0;  /* must be 0: held the removed multi-row wave variant's
+                       block-rows per wave; nonzero is SPMM_INVALID */
+    int reserved1;  /* must be 0: held the removed split-K wave variant;
+                       nonzero is SPMM_INVALID */
     int addressing; /* 0: B rows / A blocks as buffer records where they fit
                        (N % 8 == 0, 16-byte aligned B); 1: pointer-arithmetic
                        wave kernel */

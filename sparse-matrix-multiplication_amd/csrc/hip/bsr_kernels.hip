@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <initializer_list>
 #include <type_traits>
 
 #include "engine.h"
@@ -1108,6 +1109,27 @@ Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t strea
     if (o.row_group != 0 && o.row_group != 1 && o.row_group != 4 && o.row_group != 8) {
         return fail(kInvalid, "row_group must be 0, 1, 4 or 8");
     }
+    // Option values no kernel has are refused; with the kernel chosen
+    // explicitly (row_group 1 / per_wave, row_group 4 / 8) so are the values
+    // that kernel lacks.  Under the automatic choice a value the chosen kernel
+    // lacks takes that kernel's default.
+    const auto one_of = [](int v, std::initializer_list<int> ok) {
+        for (int x : ok) {
+            if (v == x) return true;
+        }
+        return false;
+    };
+    if (!one_of(o.tiles, {0, 1, 2, 4, 8}) || !one_of(o.depth, {0, 1, 2, 4})) {
+        return fail(kInvalid, "tiles must be 0, 1, 2, 4 or 8 and depth 0, 1, 2 or 4");
+    }
+    const bool panel_forced = !o.per_wave && (o.row_group == 4 || o.row_group == 8);
+    const bool wave_forced = o.per_wave || o.row_group == 1;
+    if (panel_forced && (!one_of(o.tiles, {0, 4, 8}) || !one_of(o.depth, {0, 2, 4}))) {
+        return fail(kInvalid, "shared-panel kernel: tiles must be 0, 4 or 8 and depth 0, 2 or 4");
+    }
+    if (wave_forced && o.tiles == 8) {
+        return fail(kInvalid, "wave kernel: tiles must be 0, 1, 2 or 4");
+    }
     args.xcd_order = o.xcd_order == 2 ? 0 : 1;
     hipError_t e;
     const bool rec = o.addressing != 1 && records_fit(args);
@@ -1124,7 +1146,7 @@ Error launch_bsr(const BSR& A, const half* B, float* C, int N, hipStream_t strea
     if (panel) {
         const int R = o.row_group == 8 ? 8 : 4;
         const int j = o.tiles == 8 ? 8 : 4;
-        const int d = o.depth == 4 ? 4 : 2;
+        const int d = o.depth == 4 ? 4 : 2;  // 0 (or a wave-only 1 when automatic): 2
         if (R == 4) {
             e = j == 4 ? dispatch_panel<4, 4>(d, args, stream) : dispatch_panel<4, 8>(d, args, stream);
         } else {

@@ -61,19 +61,29 @@ struct TileArgs {
 };
 
 // Swizzle of a staged B row's 16-byte chunks: chunk c of staged row r sits at
-// position c ^ swz(r).  A ds_read_b64_tr_b16 is served 16 lanes (128 bytes)
-// per pass; the 16 lanes of a pass address four rows r0 .. r0+3 (r0 a
-// multiple of 4), four lanes per row covering two adjacent chunk positions.
-// With rows of CH >= 8 chunks every row starts on bank 0 (mod 32 banks), so
-// the four rows need four different even offsets: swz(r) = 2 (r & 3).  With
-// CH = 4 two rows share a 128-byte bank line, so rows of one parity need two
-// different offsets: swz(r) = 2 ((r >> 1) & 1).  (An earlier swizzle,
-// 2 ((r >> 1) ^ (r >> 3)), gave two rows of a pass the same offset: two
-// conflict cycles on top of the four each read takes, rocprofv3
-// SQ_LDS_BANK_CONFLICT against SQ_LDS_IDX_ACTIVE.)
+// position c ^ swz(r).  The LDS has 64 four-byte banks (256 bytes per pass)
+// and serves a ds_read_b64_tr_b16 in two passes of 32 lanes.  The four lanes
+// of a row read 32 contiguous bytes (eight banks), so a pass is conflict-free
+// when its eight rows land on eight different 8-bank groups.  A pair read
+// (rows 8g + t/4, or + 4) puts rows r0 .. r0+3 and r0+8 .. r0+11 in a pass,
+// a 16-deep read (rows 4g + t/4) rows r0 .. r0+7 (r0 a multiple of 16, or of
+// 4 / 8 for the upper sets).  A row is 16 CH bytes, so 16 / CH rows share a
+// 256-byte bank line and rows r, r' of a pass start on the same bank when
+// r = r' mod 16 / CH; the swizzle moves a row's reads by s(r) = swz(r) / 2
+// 32-byte units, and such rows need different s.  With x = bit 2 ^ bit 3 of
+// r: s = x (CH = 4), s = bit 1 | x << 1 (CH = 8), s = (r & 3) | x << 2
+// (CH = 16).  The period is 16 rows.
+// (Swizzles built for 32 banks and 16-lane passes, 2 (r & 3) for CH >= 8 and
+// 2 ((r >> 1) & 1) for CH = 4, left two rows of every pass on one group:
+// two conflict cycles per read, rocprofv3 SQ_LDS_BANK_CONFLICT = 2 x
+// SQ_INSTS_LDS.)
 template <int CH>
 __device__ __forceinline__ int tile_swz(int r) {
-    return CH >= 8 ? 2 * (r & 3) : CH == 4 ? 2 * ((r >> 1) & 1) : 0;
+    const int x = ((r >> 2) ^ (r >> 3)) & 1;
+    return CH >= 16 ? 2 * ((r & 3) | (x << 2))
+         : CH == 8  ? 2 * (((r >> 1) & 1) | (x << 1))
+         : CH == 4  ? 2 * x
+                    : 0;
 }
 
 // Workgroup -> (panel, column tile).  The hardware hands workgroup L to XCD
@@ -381,10 +391,12 @@ __global__ __launch_bounds__(256) void bsr_tile_kernel(TileArgs a) {
 
 // ---------------------------------------------------------------------------
 // Producer / consumer form (the whole union of a panel in LDS at once):
-// eight waves, waves 4..7 only issue buffer-to-LDS loads of the panel's A
-// blocks and B rows, chunk by chunk, and waves 0..3 only multiply, so the
-// multiplication of chunk k overlaps the loads of the chunks after it and
-// no multiplying wave ever waits for the vector-memory issue queue.  One
+// NC + NP waves, waves NC .. NC+NP-1 only issue buffer-to-LDS loads of the
+// panel's A blocks and B rows, chunk by chunk, and waves 0 .. NC-1 only
+// multiply, so the multiplication of chunk k overlaps the loads of the
+// chunks after it and no multiplying wave ever waits for the vector-memory
+// issue queue (the launcher runs four of each: one or two producers, or
+// eight consumers on twice the rows or columns, measured slower).  One
 // workgroup barrier per chunk: a producer passes barrier k once its own
 // loads of chunk k have landed, a consumer passes it before multiplying
 // chunk k.
@@ -397,20 +409,20 @@ __global__ __launch_bounds__(256) void bsr_tile_kernel(TileArgs a) {
 //   slot.  When the wave's block-rows share their run, a pair's B operand is
 //   read once for all of them.
 // ---------------------------------------------------------------------------
-template <int R, int NT, int WC, int CS, int NB>
+template <int R, int NT, int WC, int CS, int NB, bool AV, int NC, int NP>
 __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict__ Bs,
                                         _Float16* __restrict__ As) {
-    constexpr int WR  = 4 / WC;          // consumer wave rows
+    constexpr int WR  = NC / WC;         // consumer wave rows
     constexpr int RW  = R / WR;          // block-rows per consumer wave
     constexpr int TC  = NT / 16 / WC;    // 16-column tiles per consumer wave
     constexpr int CH  = NT / 8;          // 16-byte chunks per staged B row
     constexpr int NS  = NB * CS;         // union slots held
     constexpr int PP  = CS / 2;          // pairs completed per chunk and block-row (at most)
-    constexpr int TA  = R * CS / 2;      // A loads per chunk (two blocks each)
+    constexpr int TA  = AV ? 0 : R * CS / 2;  // A loads per chunk (two blocks each)
     constexpr int TBL = CS * 16 * CH / 64;  // B loads per chunk
-    constexpr int LPP = (TA + TBL) / 4;  // loads per producer wave per chunk
-    static_assert(WR * WC == 4 && R % WR == 0 && TC >= 1, "wave grid");
-    static_assert(CS % 2 == 0 && (TA + TBL) % 4 == 0, "chunk shape");
+    constexpr int LPP = (TA + TBL) / NP;  // loads per producer wave per chunk
+    static_assert(WR * WC == NC && R % WR == 0 && TC >= 1, "wave grid");
+    static_assert(CS % 2 == 0 && (TA + TBL) % NP == 0, "chunk shape");
     static_assert(NB * LPP < 64, "vmcnt is 6 bits");
 
     const int lane = threadIdx.x & 63;
@@ -430,16 +442,17 @@ __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict_
     const int U  = d[1];
     const int nch = (U + CS - 1) / CS;
 
-    if (wave >= 4) {
+    if (wave >= NC) {
         // ---- producer ----
         // Producer pw loads the A blocks of block-rows pw*RP .. pw*RP+RP-1
         // (two slots per load) and every fourth B load of each chunk.  Its
         // lane constants do not depend on the chunk: a chunk is CS*16 staged
         // rows, a multiple of the swizzle's period.
-        constexpr int RP  = R / 4;             // block-rows per producer
-        constexpr int BPP = TBL / 4;           // B loads per producer per chunk
-        static_assert(R % 4 == 0 && TBL % 4 == 0 && (CS * 16) % 32 == 0, "producer split");
-        const int pw = wave - 4;
+        constexpr int RP  = AV ? 1 : R / NP;   // block-rows per producer (A in LDS)
+        constexpr int BPP = TBL / NP;          // B loads per producer per chunk
+        static_assert((AV || R % NP == 0) && TBL % NP == 0 && (CS * 16) % 32 == 0,
+                      "producer split");
+        const int pw = wave - NC;
         int lo[RP], hi[RP], ab[RP];
 #pragma unroll
         for (int q = 0; q < RP; ++q) {
@@ -458,7 +471,7 @@ __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict_
         int b_sr[BPP], b_nbyte[BPP];
 #pragma unroll
         for (int s = 0; s < BPP; ++s) {
-            const int piece = (4 * s + pw) * 64 + lane;
+            const int piece = (NP * s + pw) * 64 + lane;
             b_sr[s] = piece / CH;  // staged row inside the chunk
             const int n = n0 + ((piece % CH) ^ tile_swz<CH>(b_sr[s])) * 8;
             b_nbyte[s] = (n < a.N ? n : 0) * 2;
@@ -468,7 +481,7 @@ __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict_
         // the consumers' 16-byte operand reads conflict-free.
         auto issue = [&](int k) {
 #pragma unroll
-            for (int q = 0; q < RP; ++q) {
+            for (int q = 0; q < (AV ? 0 : RP); ++q) {
 #pragma unroll
                 for (int m = 0; m < CS / 2; ++m) {
                     const int v0 = k * CS + 2 * m;
@@ -482,7 +495,7 @@ __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict_
             for (int s = 0; s < BPP; ++s) {
                 const int rs  = k * CS * 16 + b_sr[s];  // staged row inside the panel
                 const int row = rs < U * 16 ? u0 * 16 + rs : -1;
-                lds_dma_x4(words_b, bs_base + (k * CS * 16 * NT + 4 * s * 512) * 2, row,
+                lds_dma_x4(words_b, bs_base + (k * CS * 16 * NT + NP * s * 512) * 2, row,
                            b_nbyte[s]);
             }
         };
@@ -492,14 +505,19 @@ __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict_
         // barrier, so the consumers start on chunk 0 while later chunks are
         // still being issued.
         constexpr int kLook = 2;
+        // (later < NB, so later * LPP < 64; the clamp only keeps the
+        // unreachable cases' template arguments in range)
+        constexpr int L1 = LPP < 64 ? LPP : 0, L2 = 2 * LPP < 64 ? 2 * LPP : 0;
+        constexpr int L3 = 3 * LPP < 64 ? 3 * LPP : 0, L4 = 4 * LPP < 64 ? 4 * LPP : 0;
+        constexpr int L5 = 5 * LPP < 64 ? 5 * LPP : 0;
         auto wait_chunks_out = [&](int later) {
             switch (later) {
                 case 0: wait_vmcnt<0>(); break;
-                case 1: wait_vmcnt<LPP>(); break;
-                case 2: wait_vmcnt<2 * LPP>(); break;
-                case 3: wait_vmcnt<3 * LPP>(); break;
-                case 4: wait_vmcnt<4 * LPP>(); break;
-                default: wait_vmcnt<(NB >= 6 ? 5 * LPP : 0)>(); break;
+                case 1: wait_vmcnt<L1>(); break;
+                case 2: wait_vmcnt<L2>(); break;
+                case 3: wait_vmcnt<L3>(); break;
+                case 4: wait_vmcnt<L4>(); break;
+                default: wait_vmcnt<(NB >= 6 ? L5 : 0)>(); break;
             }
         };
 #pragma unroll
@@ -534,6 +552,50 @@ __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict_
     bool shared = true;
 #pragma unroll
     for (int i = 1; i < RW; ++i) shared = shared && lo[i] == lo[0] && hi[i] == hi[0];
+    // Pairs of block-row i completed by chunk k: [P(k), P(k+1)), P(k) = the
+    // pairs whose second slot lies below slot k*CS.
+    auto pairs_below = [&](int i, int slot) {
+        const int x = slot >= lo[i] ? (slot - lo[i]) >> 1 : 0;
+        return min(x, (hi[i] - lo[i]) >> 1);
+    };
+    // AV: the A operands come straight from global memory into VGPRs, all of
+    // them before the first barrier: per chunk k, pair slot pp and block-row
+    // i the 16x32 operand of pair P(k) + pp (row t, columns 8(g&1) .. +7 of
+    // block 2p + (g>>1) of the run), index -1 (zeros, no memory access) when
+    // the chunk completes fewer pairs; and per block-row the 16x16 operand of
+    // an odd run's last block (row t, columns 4g .. 4g+3: the low half of a
+    // 16-byte load at column 4g, or the high half of the load at column 8 for
+    // g = 3, which keeps the load inside the block).  A consumer issues no
+    // other loads, so the compiler's waits on them are exact.
+    u32x4 avg[AV ? NB : 1][PP][RW];
+    u32x4 avt[RW];
+    if constexpr (AV) {
+        const __amdgpu_buffer_rsrc_t rec_a = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<_Float16*>(a.vals), static_cast<short>(512), a.num_blocks, kBufWord3);
+        const int off_full = t * 32 + 16 * (g & 1);
+        const int off_half = t * 32 + (g < 3 ? 8 * g : 16);
+        int ab[RW];
+#pragma unroll
+        for (int i = 0; i < RW; ++i) ab[i] = d[2 + 2 * R + wr * RW + i];
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+#pragma unroll
+            for (int i = 0; i < RW; ++i) {
+                const int p0 = pairs_below(i, k * CS), p1 = pairs_below(i, (k + 1) * CS);
+#pragma unroll
+                for (int pp = 0; pp < PP; ++pp) {
+                    const int p = p0 + pp;
+                    const int idx = p < p1 ? ab[i] + 2 * p + (g >> 1) : -1;
+                    avg[k][pp][i] = sbuf_load_u32x4(rec_a, idx, off_full, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RW; ++i) {
+            const int cnt = hi[i] - lo[i];
+            avt[i] = sbuf_load_u32x4(rec_a, (cnt & 1) ? ab[i] + cnt - 1 : -1, off_half, 0, 0);
+        }
+    }
 
     f32x4 acc[RW][TC];
 #pragma unroll
@@ -562,12 +624,6 @@ __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict_
     auto a_read4 = [&](int byte) -> f16x4 {
         return *reinterpret_cast<const f16x4*>(reinterpret_cast<const char*>(As) + byte);
     };
-    // Pairs of block-row i completed by chunk k: [P(k), P(k+1)), P(k) = the
-    // pairs whose second slot lies below slot k*CS.
-    auto pairs_below = [&](int i, int slot) {
-        const int x = slot >= lo[i] ? (slot - lo[i]) >> 1 : 0;
-        return min(x, (hi[i] - lo[i]) >> 1);
-    };
     auto compute = [&](int k) {
         if (shared) {
             const int p0 = pairs_below(0, k * CS), p1 = pairs_below(0, (k + 1) * CS);
@@ -586,7 +642,13 @@ __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict_
                     bf[pp][j] = __builtin_bit_cast(f16x8, both);
                 }
 #pragma unroll
-                for (int i = 0; i < RW; ++i) af[pp][i] = a_read8(((wr * RW + i) * NS + u) * 512 + a_pair);
+                for (int i = 0; i < RW; ++i) {
+                    if constexpr (AV) {
+                        af[pp][i] = __builtin_bit_cast(f16x8, avg[k][pp][i]);
+                    } else {
+                        af[pp][i] = a_read8(((wr * RW + i) * NS + u) * 512 + a_pair);
+                    }
+                }
             }
 #pragma unroll
             for (int pp = 0; pp < PP; ++pp) {
@@ -615,7 +677,11 @@ __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict_
                         const s16x8 both = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
                         bf[pp][j] = __builtin_bit_cast(f16x8, both);
                     }
-                    af[pp] = a_read8(((wr * RW + i) * NS + u) * 512 + a_pair);
+                    if constexpr (AV) {
+                        af[pp] = __builtin_bit_cast(f16x8, avg[k][pp][i]);
+                    } else {
+                        af[pp] = a_read8(((wr * RW + i) * NS + u) * 512 + a_pair);
+                    }
                 }
 #pragma unroll
                 for (int pp = 0; pp < PP; ++pp) {
@@ -633,7 +699,13 @@ __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict_
         for (int i = 0; i < RW; ++i) {
             const int v = hi[i] - 1;
             if (((hi[i] - lo[i]) & 1) && v >= k * CS && v < (k + 1) * CS) {
-                const f16x4 av = a_read4(((wr * RW + i) * NS + v) * 512 + a_one);
+                f16x4 av;
+                if constexpr (AV) {
+                    const u32x4 w = avt[i];
+                    av = __builtin_bit_cast(f16x4, g < 3 ? u32x2{w[0], w[1]} : u32x2{w[2], w[3]});
+                } else {
+                    av = a_read4(((wr * RW + i) * NS + v) * 512 + a_one);
+                }
 #pragma unroll
                 for (int j = 0; j < TC; ++j) {
                     const f16x4 bv = __builtin_bit_cast(f16x4, b_read(16 * v + r_h, wc * TC + j));
@@ -670,21 +742,21 @@ __device__ __forceinline__ void pc_body(const TileArgs& a, _Float16* __restrict_
     }
 }
 
-template <int R, int NT, int WC, int CS, int NB>
-__global__ __launch_bounds__(512) void bsr_tile_pc_kernel(TileArgs a) {
+template <int R, int NT, int WC, int CS, int NB, bool AV, int NC, int NP>
+__global__ __launch_bounds__(64 * (NC + NP)) void bsr_tile_pc_kernel(TileArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 Bs[NB * CS * 16 * NT];
-    __shared__ __attribute__((aligned(16))) _Float16 As[R * NB * CS * 256];
-    pc_body<R, NT, WC, CS, NB>(a, Bs, As);
+    __shared__ __attribute__((aligned(16))) _Float16 As[AV ? 8 : R * NB * CS * 256];
+    pc_body<R, NT, WC, CS, NB, AV, NC, NP>(a, Bs, As);
 }
 
-template <int R, int NT, int WC, int CS, int NB>
+template <int R, int NT, int WC, int CS, int NB, bool AV, int NC, int NP>
 hipError_t run_tile_pc(TileArgs args, int panels, hipStream_t stream) {
     args.tiles_n = (args.N + NT - 1) / NT;
     const long total = static_cast<long>(panels) * args.tiles_n;
     if (total > 0x7fffffffL) return hipErrorInvalidConfiguration;
     args.wg_total = static_cast<int>(total);
-    hipLaunchKernelGGL((bsr_tile_pc_kernel<R, NT, WC, CS, NB>), dim3(args.wg_total), dim3(512), 0,
-                       stream, args);
+    hipLaunchKernelGGL((bsr_tile_pc_kernel<R, NT, WC, CS, NB, AV, NC, NP>), dim3(args.wg_total),
+                       dim3(64 * (NC + NP)), 0, stream, args);
     return hipGetLastError();
 }
 
@@ -701,23 +773,37 @@ hipError_t run_tile(TileArgs args, int panels, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// One launcher per shape, instantiating only the kernel its kind names.
+template <int R, int NT, int WC, int CS, int NB, int KIND>
+hipError_t run_shape(TileArgs args, int panels, hipStream_t stream) {
+    if constexpr (KIND >= 2) {
+        return run_tile_pc<R, NT, WC, CS, NB, KIND == 3, 4, 4>(args, panels, stream);
+    } else {
+        return run_tile<R, NT, WC, CS, NB, KIND == 1>(args, panels, stream);
+    }
+}
+
 }  // namespace
 
 int tile_shape_count() { return static_cast<int>(sizeof(kTileShapes) / sizeof(kTileShapes[0])); }
 
 // Measured on MI355X (c3: banded 8192^2 half-bandwidth 64, N = 128; c4:
 // block-diagonal 32 x 256^2, N = 256; per launch, back to back): the producer
-// / consumer form beats the forms with A in VGPRs, and 32 (N <= 128) or 64
-// columns per workgroup beat wider tiles, whose fewer workgroups leave CUs
-// idle or hide less latency (c3 3.35 us at 32 columns, 3.42 at 64, 4.9 at
-// 128; c4 4.52 us at 64, 5.3 at 128).  Unions wider than the one-shot forms
-// hold take the ring.
+// / consumer forms beat the forms whose multiplying waves also issue the
+// loads, and 32 (N <= 128) or 64 columns per workgroup beat wider tiles,
+// whose fewer workgroups overlap less of each workgroup's load -> multiply
+// -> store chain (c3 3.24 us at 32 columns, 3.30 at 64, 4.2 at 128; c4 4.34
+// us at 64, 4.7 - 5.3 at 128, also with eight multiplying waves).  At 32
+// columns consumers loading their A operands straight into VGPRs (KIND 3)
+// win (c3 3.24 against 3.32 with A staged in LDS); at 64 columns on c4 A in
+// LDS (KIND 2) does (4.34 against 4.48).  Unions wider than the one-shot
+// forms hold take the ring.
 int default_tile_shape(int R, int max_union, int M, int N) {
     const auto fits = [&](int id) {
         return kTileShapes[id].NB * kTileShapes[id].CS >= max_union;
     };
     if (R == 8) return fits(0) ? 0 : 11;
-    if (N <= 128) return fits(5) ? 5 : fits(12) ? 12 : 10;
+    if (N <= 128) return fits(14) ? 14 : fits(15) ? 15 : 10;
     return fits(3) ? 3 : 10;
 }
 
@@ -869,11 +955,8 @@ Error launch_bsr_tile(const BsrTilePlan& plan, const BSR& A, const half* B, floa
                   A.num_blocks};
     hipError_t e = hipSuccess;
     switch (shape) {
-#define SPMM_TILE_CASE(ID, R_, NT_, WC_, CS_, NB_, KIND_)                                   \
-    case ID:                                                                                  \
-        e = KIND_ == 2 ? run_tile_pc<R_, NT_, WC_, CS_, NB_>(args, plan.panels, stream)      \
-                       : run_tile<R_, NT_, WC_, CS_, NB_, KIND_ == 1>(args, plan.panels, stream); \
-        break;
+#define SPMM_TILE_CASE(ID, R_, NT_, WC_, CS_, NB_, KIND_) \
+    case ID: e = run_shape<R_, NT_, WC_, CS_, NB_, KIND_>(args, plan.panels, stream); break;
         SPMM_TILE_SHAPES(SPMM_TILE_CASE)
 #undef SPMM_TILE_CASE
         default: return fail(kInvalid, "unknown tile shape");

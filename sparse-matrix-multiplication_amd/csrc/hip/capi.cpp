@@ -788,6 +788,11 @@ int spmm_c_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B16, float* d_C,
     if (d_bsr == nullptr) return set_error(SPMM_INVALID, "null matrix descriptor");
     spmm::engine::BsrOpts o;
     if (opts != nullptr) {
+        if (opts->reserved0 != 0 || opts->reserved1 != 0) {
+            return set_error(SPMM_INVALID,
+                             "spmm_bsr_opts_t reserved fields must be 0 (the multi-row and "
+                             "split-K wave variants were removed)");
+        }
         o.row_group = opts->row_group;
         o.tiles     = opts->tiles;
         o.per_wave  = opts->per_wave;

@@ -117,7 +117,8 @@ struct BsrTilePlan {
 // per staged chunk, NB chunk buffers, KIND).  KIND 0: A operands in VGPRs, a
 // ring of NB B buffers with NB - 1 chunks in flight (any union width); 1: A
 // in VGPRs, the whole union in flight (widest union <= NB * CS); 2: producer
-// and consumer waves, A and B staged in LDS, the whole union in flight.
+// and consumer waves, A and B staged in LDS, the whole union in flight; 3: as
+// 2 with the consumers loading their A operands straight into VGPRs.
 struct TileShape {
     int R, NT, WC, CS, NB, KIND;
 };
@@ -134,7 +135,11 @@ struct TileShape {
     X(9, 4, 128, 2, 4, 5, 0)     \
     X(10, 4, 64, 1, 4, 4, 0)     \
     X(11, 8, 64, 1, 4, 5, 0)     \
-    X(12, 4, 32, 1, 4, 4, 2)
+    X(12, 4, 32, 1, 4, 4, 2)     \
+    X(13, 4, 64, 1, 4, 4, 3)     \
+    X(14, 4, 32, 1, 4, 3, 3)     \
+    X(15, 4, 32, 1, 4, 4, 3)     \
+    X(16, 8, 64, 1, 4, 4, 3)
 #define SPMM_TILE_ENTRY(ID, R_, NT_, WC_, CS_, NB_, KIND_) TileShape{R_, NT_, WC_, CS_, NB_, KIND_},
 constexpr TileShape kTileShapes[] = {SPMM_TILE_SHAPES(SPMM_TILE_ENTRY)};
 #undef SPMM_TILE_ENTRY

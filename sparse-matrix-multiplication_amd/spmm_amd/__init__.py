@@ -75,6 +75,7 @@ class EngineOptsT(ctypes.Structure):
 class BsrOptsT(ctypes.Structure):
     _fields_ = [("row_group", ctypes.c_int), ("tiles", ctypes.c_int), ("per_wave", ctypes.c_int),
                 ("depth", ctypes.c_int), ("xcd_order", ctypes.c_int),
+                ("reserved0", ctypes.c_int), ("reserved1", ctypes.c_int),
                 ("addressing", ctypes.c_int)]
 
 

@@ -112,5 +112,5 @@ def test_shapes_table(S):
     shapes = S.bsr_tile_shapes()
     assert shapes, "no kernel shapes"
     for sh in shapes:
-        assert sh["R"] in (4, 8) and sh["KIND"] in (0, 1, 2)
+        assert sh["R"] in (4, 8) and sh["KIND"] in (0, 1, 2, 3)
         assert sh["NT"] % 16 == 0 and sh["CS"] % 2 == 0 and 2 <= sh["NB"] <= 6

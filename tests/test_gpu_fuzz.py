@@ -130,10 +130,10 @@ def test_mfma_random(S, O, torch, chunk):
         kernel = int(rng.choice([0, 1, 4, 8]))  # automatic, wave, panel R = 4 / 8
         if kernel == 1:
             opts = S.BsrOptsT(1, int(rng.choice([0, 1, 2, 4])), 1, int(rng.choice([0, 1, 2, 4])),
-                              int(rng.choice([0, 1, 2])), int(rng.choice([0, 1])))
+                              int(rng.choice([0, 1, 2])), addressing=int(rng.choice([0, 1])))
         else:
-            opts = S.BsrOptsT(kernel, int(rng.choice([0, 4, 8])), 0, int(rng.choice([0, 2, 3, 4])),
-                              int(rng.choice([0, 1, 2])), 0)
+            opts = S.BsrOptsT(kernel, int(rng.choice([0, 4, 8])), 0, int(rng.choice([0, 2, 4])),
+                              int(rng.choice([0, 1, 2])))
         say(f"fuzz mfma chunk={chunk} case={case} M={M} K={K} N={N} blocks={hb.num_blocks} "
             f"opts=(row_group {opts.row_group}, tiles {opts.tiles}, depth {opts.depth}, "
             f"order {opts.xcd_order}, addressing {opts.addressing})")

@@ -82,7 +82,12 @@ def test_hybrid_picks_faster_backend(S, cfg):
     t_csr = _batch_us(torch, csr_launch)
     dAb = S.DeviceBSR(S.bsr_from_csr_host(A))
     B16 = S.float_to_half(dB)
-    t_mma = _batch_us(torch, lambda n: S.launch_repeat("wmma", dAb, B16, dC, n))
+    try:  # the run-panel form on structured matrices, else the record kernel
+        tile = S.BsrTilePlan(dAb)
+        t_mma = _batch_us(torch, lambda n: tile.launch_repeat(B16, dC, n))
+    except S.SpmmError as e:
+        assert e.code == S.SPMM_UNSUPPORTED
+        t_mma = _batch_us(torch, lambda n: S.launch_repeat("wmma", dAb, B16, dC, n))
     print(f"hybrid config={cfg} csr({form})_us={t_csr:.2f} wmma_us={t_mma:.2f} "
           f"plan={plan.backend_name}", flush=True)
     if max(t_csr, t_mma) <= 1.10 * min(t_csr, t_mma):

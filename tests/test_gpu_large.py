@@ -57,7 +57,9 @@ def _sample_ref(A, B, rows):
 def _csr_launch(S, torch, A, dA, dB, C):
     form, opts, parts = S.csr_auto_form(A, int(dB.shape[1]))
     stream = torch.cuda.current_stream()
-    if form == "split":
+    if form == "khalf":
+        S.KHalfPlan(A, int(dB.shape[1])).launch_repeat(dB, C, 1, stream)
+    elif form == "split":
         rows = torch.from_numpy(S.nnz_split_rows(A, parts)).cuda()
         carry = torch.empty((parts, dB.shape[1]), dtype=torch.float32, device="cuda")
         S.launch_repeat_split(dA, rows, dB, C, carry, 1, stream)

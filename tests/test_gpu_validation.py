@@ -109,6 +109,11 @@ def test_bsr_operands_rejected(S):
     _rejects(S, lambda: S.spmm_wmma_opts(dA, B16.t(), S.BsrOptsT(), C), C)   # non-contiguous
     _rejects(S, lambda: S.launch_repeat_wmma_opts(dA, B16, C[:32], S.BsrOptsT(), 2), C)
     _rejects(S, lambda: S.launch_repeat("wmma", dA, B32, C, 2), C)
+    # option values no kernel has, values the named kernel lacks (panel depth
+    # 3, panel tiles 2, wave tiles 8) and nonzero reserved slots
+    for opts in (S.BsrOptsT(4, 4, 0, 3), S.BsrOptsT(8, 2, 0, 2), S.BsrOptsT(1, 8, 0, 2),
+                 S.BsrOptsT(0, 0, 0, 8), S.BsrOptsT(reserved0=1), S.BsrOptsT(reserved1=4)):
+        _rejects(S, lambda: S.spmm_wmma_opts(dA, B16, opts, C), C)
     # a correct call still works
     S.spmm_wmma(dA, B16, C)
     torch.cuda.synchronize()

@@ -21,7 +21,14 @@ c2 18.9 against 17.1 us, c1 8.0 against 5.9, c5 64.5 against 59.7; the
 shader clock is already at 2.4 GHz, a copy kernel run first does not shorten
 it, 2000 launches of the same step do), so
 each block also carries `steady`: the same step after at least 0.1 s of
-untimed launches, 500 timed, measured afterwards.  `cold_ms_median` is the median of
+untimed launches, 500 timed, measured afterwards.  The gap is the shader
+clock: `sclk_mhz` is the median shader clock the GPU delivers over the 200
+launches right after the timed steps (and after the steady ones), sampled
+every 5 us by a one-wave trace on a second stream (shader cycles against the
+100 MHz real-time counter).  Under this load it starts near 2.1 GHz after
+idle and reaches about 2.38 GHz only after ~1000 back-to-back launches while
+the DPM state already reads 2.4 GHz (`--ramp c2,c1` prints time and clock per
+batch of 20 launches from a fresh start).  `cold_ms_median` is the median of
 single launches each preceded by a 512 MiB write that evicts L2 (4 MiB per
 XCD) and the 256 MB MALL; warm is the contract figure.  `graph_ms_per_step`
 is the same launches captured 100 at a time in one HIP graph and replayed (a
@@ -218,6 +225,60 @@ def time_warm(torch, P, steps: int) -> float:
     return ev0.elapsed_time(ev1) / steps
 
 
+def clock_during(torch, S, P, launches: int, est_ms: float, interval_us: float = 5.0):
+    """Median shader clock (MHz) the GPU delivers over `launches` back-to-back
+    launches of the step: a one-wave trace on a second stream samples shader
+    cycles against the 100 MHz real-time counter every `interval_us` while the
+    launches run (S.shader_clock_trace).  Untimed."""
+    side = torch.cuda.Stream()
+    span_us = launches * est_ms * 1e3
+    samples = int(span_us / interval_us) + 2
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        out = S.shader_clock_trace(samples, interval_us)
+    P["launch"](launches)
+    torch.cuda.synchronize()
+    vals = [mhz for t, mhz in S.shader_clock_series(out) if t <= span_us]
+    return round(_median(vals), 1) if vals else None
+
+
+def ramp(torch, S, name: str, idle_s: float = 1.0, batches: int = 150, per: int = 20) -> dict:
+    """Warm-up ramp of one pattern from this process's first launches: after
+    one launch and `idle_s` seconds idle, `batches` batches of `per`
+    back-to-back launches, each timed between two events while a one-wave
+    shader-clock trace on a second stream samples the clock every 5 us (the
+    batch's figure is the median over its intervals)."""
+    P = build_pattern(S, torch, name)
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    P["launch"](1)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    est_us = e0.elapsed_time(e1) * 1e3
+    time.sleep(idle_s)
+    side = torch.cuda.Stream()
+    us, mhz = [], []
+    for _ in range(batches):
+        span = est_us * per
+        with torch.cuda.stream(side):
+            out = S.shader_clock_trace(int(span / 5.0) + 2, 5.0)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        P["launch"](per)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        batch_us = e0.elapsed_time(e1) * 1e3
+        vals = [m for t, m in S.shader_clock_series(out) if t <= batch_us]
+        us.append(round(batch_us / per, 3))
+        mhz.append(round(_median(vals), 1) if vals else None)
+        est_us = batch_us / per
+    return {"ramp": name, "form": P["form"], "idle_s": idle_s, "launches_per_batch": per,
+            "us_per_launch": us, "sclk_mhz": mhz}
+
+
 def time_cold(torch, P, flush, reps: int = 15) -> float:
     """Median of single launches, each after a 512 MiB write (L2 and MALL evicted)."""
     stream = torch.cuda.current_stream()
@@ -358,6 +419,10 @@ def main() -> int:
     ap.add_argument("--only", default="",
                     help="comma-separated subset of c1..c5 (profiling runs); the headline "
                          "line needs c2")
+    ap.add_argument("--ramp", default="",
+                    help="comma-separated patterns: print each one's warm-up ramp (time "
+                         "per launch and delivered shader clock per batch of 20 launches "
+                         "after 1 s idle) as one JSON line instead of the benchmark")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 256 MiB device-to-device copy, --steps times (the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -378,6 +443,10 @@ def main() -> int:
     assert torch.cuda.is_available(), "bench.py needs an MI355X"
     torch.cuda.set_device(0)
     S.lib()
+    if args.ramp:
+        for name in args.ramp.split(","):
+            print(json.dumps(ramp(torch, S, name)), flush=True)
+        return 0
 
     flush = None if args.no_cold else torch.empty(FLUSH_BYTES // 4, dtype=torch.float32,
                                                   device="cuda")
@@ -386,9 +455,11 @@ def main() -> int:
         P = build_pattern(S, torch, name)
         warmed = warm_up(torch, P, args.warmup)
         ms = time_warm(torch, P, args.steps)
+        sclk = {"next_200_launches": clock_during(torch, S, P, 200, ms)}
         cold = time_cold(torch, P, flush) if flush is not None else None
         blk, flops = pattern_block(P, ms, cold)
         blk["warmup_steps"] = warmed
+        blk["sclk_mhz"] = sclk
         if not args.no_graph:
             gms, why = time_graph(torch, P)
             blk["graph_ms_per_step"] = None if gms is None else round(gms, 6)
@@ -400,6 +471,7 @@ def main() -> int:
             # afterwards and reported beside it (never as ms_per_step or value).
             sw = warm_up(torch, P, None)
             sms = time_warm(torch, P, STEADY_STEPS)
+            sclk["after_steady_next_200"] = clock_during(torch, S, P, 200, sms)
             blk["steady"] = {"ms_per_step": round(sms, 6),
                              "gflops": round(flops / (sms * 1e-3) / 1e9, 2),
                              "warmup_steps": sw, "steps": STEADY_STEPS}

@@ -372,6 +372,14 @@ int spmm_c_launch_repeat_bsr_tile(const spmm_bsr_tile_plan_t* plan, const spmm_b
 int spmm_c_time_repeat(int kernel_id, const void* d_A_any, const void* d_B, float* d_C,
                        int N, int reps, void* stream, float* ms_out);
 int spmm_c_device_synchronize(void);
+/* Shader-clock trace (no reference counterpart; a timing diagnostic): one
+ * wave enqueued on `stream` writes the shader-cycle count and the 100 MHz
+ * real-time tick count `samples` (2 .. 2^20) times, `interval_ticks`
+ * (1 .. 1e8) ticks apart, to d_out[2i] and d_out[2i + 1] (d_out: 2 * samples
+ * uint64), and ends after at most 60 s.  Launched on a second stream beside
+ * a workload, 100 * dcycles / dticks is the shader clock in MHz that the
+ * workload ran at during interval i. */
+int spmm_c_shader_clock_trace(uint64_t* d_out, int samples, int interval_ticks, void* stream);
 
 #ifdef __cplusplus
 }

@@ -773,6 +773,11 @@ int spmm_c_tiled_v3_opts(const spmm_csr_t* d_A, const float* d_B, float* d_C, in
                                                 d_B, d_C, N, as_stream(stream), nullptr, 0, &o));
 }
 
+int spmm_c_shader_clock_trace(uint64_t* d_out, int samples, int interval_ticks, void* stream) {
+    return from_engine(spmm::engine::launch_shader_clock_trace(
+        reinterpret_cast<unsigned long long*>(d_out), samples, interval_ticks, as_stream(stream)));
+}
+
 int spmm_c_float_to_half(const float* d_src, uint16_t* d_dst, long n, void* stream) {
     return from_engine(spmm::engine::launch_float_to_half(d_src, reinterpret_cast<half*>(d_dst),
                                                           n, as_stream(stream)));

@@ -79,6 +79,12 @@ Error launch_csr(CsrRole role, const CSR& d_A, const float* d_B, float* d_C, int
 
 Error launch_float_to_half(const float* d_src, half* d_dst, long n, hipStream_t stream);
 
+// Shader-clock trace (clock.hip): one wave writes (shader cycles, 100 MHz
+// ticks) `samples` times, `interval_ticks` apart, to d_out[2i], d_out[2i+1];
+// the delivered MHz of interval i is 100 * dcycles / dticks.
+Error launch_shader_clock_trace(unsigned long long* d_out, int samples, int interval_ticks,
+                                hipStream_t stream);
+
 // Tuning of the BSR matrix-core kernels.  All zero selects the default: the
 // shared-panel kernel on wide B with long structured block-rows (N >= 256, 24
 // - 64 blocks per block-row), else the wave kernel, with shapes from N.

@@ -162,6 +162,7 @@ _SIGNATURES = {
     "spmm_c_launch_repeat_opts": (_int, [_P(CsrT), _vp, _vp, _int, _P(EngineOptsT), _int, _vp]),
     "spmm_c_time_repeat": (_int, [_int, _vp, _vp, _vp, _int, _int, _vp, _P(_float)]),
     "spmm_c_device_synchronize": (_int, []),
+    "spmm_c_shader_clock_trace": (_int, [_vp, _int, _int, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -932,6 +933,36 @@ def spmm_tiled_v3_opts(A: DeviceCSR, B, opts: EngineOptsT, C=None, stream=None):
     _check(lib().spmm_c_tiled_v3_opts(ctypes.byref(s), B.data_ptr(), C.data_ptr(), N,
                                       ctypes.byref(opts), _stream_handle(stream)))
     return C
+
+
+def shader_clock_trace(samples: int, interval_us: float, stream=None):
+    """Starts a shader-clock trace on `stream` (spmm_c_shader_clock_trace):
+    one wave samples shader cycles and 100 MHz real-time ticks `samples`
+    times, `interval_us` apart.  Returns the device buffer for
+    shader_clock_series; launch it on a second stream beside a workload."""
+    torch = _torch()
+    out = torch.zeros(2 * samples, dtype=torch.int64, device="cuda")
+    _check(lib().spmm_c_shader_clock_trace(out.data_ptr(), samples,
+                                           max(1, int(round(interval_us * 100))),
+                                           _stream_handle(stream)))
+    return out
+
+
+def shader_clock_series(out) -> list:
+    """[(t_us from the first sample, MHz over the interval ending there)] of a
+    finished shader_clock_trace buffer."""
+    v = out.cpu().numpy().reshape(-1, 2).astype(np.float64)
+    c, r = v[:, 0], v[:, 1]
+    return [(float((r[i] - r[0]) / 100.0), float(100.0 * (c[i] - c[i - 1]) / (r[i] - r[i - 1])))
+            for i in range(1, len(v)) if r[i] > r[i - 1]]
+
+
+def shader_clock_mhz(interval_us: float = 10.0, stream=None) -> float:
+    """The shader clock delivered now (one 10 us interval, synchronised)."""
+    torch = _torch()
+    out = shader_clock_trace(2, interval_us, stream)
+    torch.cuda.synchronize()
+    return shader_clock_series(out)[-1][1]
 
 
 def float_to_half(src, dst=None, stream=None):

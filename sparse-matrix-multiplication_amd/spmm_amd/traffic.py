@@ -99,7 +99,7 @@ def main() -> int:
     ap.add_argument("--command", default="", help="the rocprofv3 command lines, for the record")
     ap.add_argument("--out", required=True)
     a = ap.parse_args()
-    backend = a.backend or ("wmma" if a.form == "wmma" else "csr")
+    backend = a.backend or ("wmma" if a.form in ("wmma", "tile") else "csr")
     f_kib, f_step, n = per_step_kib(a.fetch, "FETCH_SIZE")
     w_kib, w_step, _ = per_step_kib(a.write, "WRITE_SIZE")
     cf, cw = copy_kib(a.copy_fetch, "FETCH_SIZE"), copy_kib(a.copy_write, "WRITE_SIZE")

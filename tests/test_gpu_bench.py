@@ -20,7 +20,7 @@ def _close(a, b, rel=1e-3):
 
 def test_bench_line_is_consistent(S, monkeypatch, capsys):
     import bench
-    monkeypatch.setattr(sys, "argv", ["bench.py", "--gpus", "1", "--only", "c2,c3", "--steps",
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--gpus", "1", "--only", "c2,c3,c4", "--steps",
                                       "20", "--warmup", "5", "--no-cpu", "--no-cold",
                                       "--no-graph"])
     assert bench.main() == 0
@@ -53,3 +53,10 @@ def test_bench_line_is_consistent(S, monkeypatch, capsys):
     assert _close(c3["roofline"]["achieved"],
                   c3["roofline"]["exec_flops"] / (c3["ms_per_step"] * 1e-3) / 1e12)
     assert "steady" in c3
+    c4 = line["patterns"]["c4"]
+    assert c3["form"] == "tile" and c4["form"] == "tile"  # the hybrid's run-panel form
+    assert c4["roofline"]["traffic"] is not None
+    for blk in line["patterns"].values():  # the delivered clock beside each timing
+        clk = blk["sclk_mhz"]
+        assert 100.0 < clk["next_200_launches"] < 3000.0
+        assert 100.0 < clk["after_steady_next_200"] < 3000.0

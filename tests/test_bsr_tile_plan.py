@@ -108,6 +108,30 @@ def test_uniform_random_is_not_runs(S):
     assert e.value.code == SPMM_UNSUPPORTED
 
 
+def test_records_random_runs(S):
+    # Seeded random run structures: the plan accepts exactly those whose panels'
+    # runs cover their union without a gap (restated in tile_cases), and then
+    # its records satisfy every invariant the kernel relies on.
+    from tile_cases import random_case, panels_contiguous
+    rng = np.random.default_rng(2024)
+    accepted = refused = 0
+    for case in range(120):
+        A, runs, M, K = random_case(S, rng)
+        hb = S.bsr_from_csr_host(A)
+        assert list(np.diff(hb.row_ptr)) == [L for _, L in runs], case
+        for R in (4, 8):
+            if panels_contiguous(runs, R):
+                rec, mu = S.bsr_tile_records(hb.row_ptr, hb.col_idx, hb.block_cols, R)
+                _check_records(hb, R, rec, mu)
+                accepted += 1
+            else:
+                with pytest.raises(S.SpmmError) as e:
+                    S.bsr_tile_records(hb.row_ptr, hb.col_idx, hb.block_cols, R)
+                assert e.value.code == SPMM_UNSUPPORTED, (case, R)
+                refused += 1
+    assert accepted >= 60 and refused >= 20, (accepted, refused)
+
+
 def test_shapes_table(S):
     shapes = S.bsr_tile_shapes()
     assert shapes, "no kernel shapes"

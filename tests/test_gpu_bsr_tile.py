@@ -121,6 +121,41 @@ def test_tile_full_configs(S, O, torch, name):
         check_csr(C, C64, absC, tol=1e-5)
 
 
+def test_tile_fuzz(S, O, torch):
+    # Seeded random run structures (tile_cases.random_case: random run starts
+    # and lengths, empty block-rows, ragged M and K) at random N (multiples of 8),
+    # every kernel shape whose union fits, R = 4 and 8, against the oracle.
+    from tile_cases import random_case, panels_contiguous
+    rng = np.random.default_rng(77)
+    shapes = S.bsr_tile_shapes()
+    done = 0
+    while done < 24:
+        A, runs, M, K = random_case(S, rng)
+        Rs = [R for R in (4, 8) if panels_contiguous(runs, R)]
+        if not Rs:
+            continue
+        N = 8 * int(rng.integers(1, 34))
+        B = S.round_to_fp16(rng.uniform(-1, 1, (K, N)).astype(np.float32))
+        hb, B16, C32, C64, absC = _refs(S, O, A, B)
+        dA = S.DeviceBSR(hb)
+        dB = torch.from_numpy(B16.view(np.int16)).cuda()
+        for R in Rs:
+            plan = S.BsrTilePlan(dA, R)
+            for sid, sh in enumerate(shapes):
+                if sh["R"] != R or (sh["KIND"] != 0 and sh["NB"] * sh["CS"] < plan.max_union):
+                    continue
+                say(f"tile fuzz case={done} M={M} K={K} N={N} blocks={hb.num_blocks} R={R} "
+                    f"shape={sid} max_union={plan.max_union}")
+                dC = torch.full((M, N), float("nan"), device="cuda")
+                plan.launch(dB, dC, shape=sid)
+                torch.cuda.synchronize()
+                C = dC.cpu().numpy()
+                check_bsr(C, C32, absC)
+                check_csr(C, C64, absC, tol=1e-5)
+            plan.close()
+        done += 1
+
+
 def test_tile_matches_wmma(S, O, torch):
     # Same products, same sums: within fp32 rounding of the record kernel.
     A, B = _case(S, "band", 512, 512, 30, 128, 11)

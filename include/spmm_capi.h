@@ -335,8 +335,11 @@ int spmm_c_hybrid_choose(const spmm_csr_t* h_A, int N, float fill_in_threshold,
 const char* spmm_c_backend_name(int backend);                    /* spmm_hybrid.h:51 */
 /* ---- unified memory on one GPU (spmm_multigpu.h:32, :54-58) ----------- */
 int spmm_c_gpu_count(void);                                                /* spmm_multigpu.h:32 */
-/* A, B, C in managed memory, prefetched, tiled_v3 engine; *prefetched_out is 0
- * when the device could not prefetch (pages then move on first touch). */
+/* A, B, C in managed memory, prefetched, tiled_v3 engine.  *prefetched_out:
+ * 1 prefetched; 0 the device could not prefetch (pages then move on first
+ * touch); -1 the device has no managed memory (MI355X with XNACK off): device
+ * allocations filled by explicit copies stand in for the managed ranges, the
+ * state a prefetch reaches, and the GPU never touches host memory. */
 int spmm_c_unified(const spmm_csr_t* h_A, const float* h_B, float* h_C, int N, int warmup,
                    int iters, float* ms_out, int* prefetched_out);     /* spmm_multigpu.h:57 */
 

@@ -882,12 +882,12 @@ int spmm_c_unified(const spmm_csr_t* h_A, const float* h_B, float* h_C, int N, i
     }
     return guarded([&] {
         float ms = 0.f;
-        bool moved = true;
+        int residency = spmm::engine::kUnifiedPrefetched;
         const int rc = from_engine(spmm::engine::run_unified(to_cpp(*h_A), h_B, h_C, N, warmup,
-                                                             iters, &ms, &moved));
+                                                             iters, &ms, &residency));
         if (rc == SPMM_OK) {
             if (ms_out) *ms_out = ms;
-            if (prefetched_out) *prefetched_out = moved ? 1 : 0;
+            if (prefetched_out) *prefetched_out = residency;
         }
         return rc;
     });

@@ -183,10 +183,17 @@ Error bsr_stats_device(const CSR& d_A, BSR_stats* out, hipStream_t stream);
 Error run_hybrid(const HybridPlan& plan, const CSR& h_A, const float* h_B, float* h_C, int N,
                  int warmup, int iters, float* ms);
 
-// Unified-memory execution (spmm_unified): *prefetched is false when the
-// device could not prefetch the managed ranges.
+// Unified-memory execution (spmm_unified).  *residency: how A, B and C
+// reached the device — managed and prefetched, managed and moved on first
+// touch (the device could not prefetch), or, on a device without managed
+// memory, device allocations filled by explicit copies.
+enum UnifiedResidency : int {
+    kUnifiedPrefetched   = 1,
+    kUnifiedFirstTouch   = 0,
+    kUnifiedDeviceCopies = -1,
+};
 Error run_unified(const CSR& h_A, const float* h_B, float* h_C, int N, int warmup, int iters,
-                  float* ms, bool* prefetched);
+                  float* ms, int* residency);
 
 // Merge-path partition of the row-block engine: part g takes nonzeros
 // [nnz*g/P, nnz*(g+1)/P) whatever rows they belong to, so a long row is shared

@@ -511,7 +511,8 @@ def _host_b(m: HostCSR, B) -> np.ndarray:
 
 def unified_run(m: HostCSR, B: np.ndarray, warmup: int = 3, iters: int = 10):
     """Reference spmm_unified (spmm_multigpu.cu:122-182): host in, host out ->
-    (C, median ms, prefetched)."""
+    (C, median ms, residency): 1 managed and prefetched, 0 managed but moved on
+    first touch, -1 no managed memory on the device (device copies instead)."""
     B = _host_b(m, B)
     N = B.shape[1]
     C = np.empty((m.num_rows, N), dtype=np.float32)
@@ -520,7 +521,7 @@ def unified_run(m: HostCSR, B: np.ndarray, warmup: int = 3, iters: int = 10):
     src = m.struct()
     _check(lib().spmm_c_unified(ctypes.byref(src), _ptr(B), _ptr(C), N, warmup, iters,
                                 ctypes.byref(ms), ctypes.byref(moved)))
-    return C, ms.value, bool(moved.value)
+    return C, ms.value, moved.value
 
 
 def hybrid_run(plan: Plan, m: HostCSR, B: np.ndarray, warmup: int = 3, iters: int = 10):

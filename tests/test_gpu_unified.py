@@ -12,17 +12,15 @@ def say(msg):
     print(msg, flush=True)
 
 
-def _managed(S):
-    """Whether the device reports managed-memory support; on a device that
-    does not, the unified path must refuse with SPMM_UNSUPPORTED."""
+def _residency(S):
+    """How the unified path placed A, B and C on this device: 1 managed and
+    prefetched, 0 managed but moved on first touch, -1 no managed memory on the
+    device (device allocations filled by explicit copies)."""
     A = S.csr_from_coo_host(16, 16, [0], [0], [1.0])
-    try:
-        S.unified_run(A, np.ones((16, 16), np.float32), warmup=0, iters=1)
-        return True
-    except S.SpmmError as e:
-        assert e.code == S.SPMM_UNSUPPORTED, e
-        assert "does not support managed memory" in str(e)
-        return False
+    C, ms, res = S.unified_run(A, np.ones((16, 16), np.float32), warmup=0, iters=1)
+    assert res in (-1, 0, 1) and ms >= 0
+    assert C[0, 0] == 1.0 and not C[1:].any()
+    return res
 
 
 def test_gpu_count(S):
@@ -30,8 +28,9 @@ def test_gpu_count(S):
 
 
 def test_unified_contract(S):
-    # either a working managed-memory path or a clean refusal (no fault, no exit)
-    say(f"unified managed-memory support: {_managed(S)}")
+    # a working path on every device: managed memory where the device has it,
+    # device copies where it does not (no fault, no exit)
+    say(f"unified residency on this device: {_residency(S)}")
 
 
 @pytest.mark.parametrize("case", ["c1", "ragged", "empty"])
@@ -45,11 +44,10 @@ def test_unified_matches_oracle(S, O, case):
     else:
         A = S.csr_from_coo_host(40, 30, [], [], [])
         B = np.ones((30, 64), np.float32)
-    if not _managed(S):
-        pytest.skip("device reports no managed memory (hipDeviceAttributeManagedMemory = 0)")
     say(f"unified case={case} M={A.num_rows} nnz={A.nnz} N={B.shape[1]}")
-    C, ms, moved = S.unified_run(A, B, warmup=1, iters=3)
-    say(f"  ms={ms:.4f} prefetched={moved}")
+    C, ms, res = S.unified_run(A, B, warmup=1, iters=3)
+    say(f"  ms={ms:.4f} residency={res}")
+    assert res in (-1, 0, 1)
     assert ms >= 0
     C64, absC = O.csr_spmm_f64(A.row_ptr, A.col_idx, A.values, B, threads=16)
     check_csr(C, C64, absC)

@@ -297,7 +297,9 @@ int spmm_c_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B_fp16, float* d
  * create: reads the device BSR's row_ptr and col_idx back (synchronises
  *   `stream`) and uploads the records; SPMM_UNSUPPORTED when the structure is
  *   not runs as above (use spmm_c_wmma then).
- * launch: d_B (num_cols x N fp16 bits) and d_C (num_rows x N fp32) 16-byte
+ * launch: d_A must carry the row_ptr / col_idx arrays the plan was created
+ *   from (SPMM_INVALID otherwise; its values may change between launches);
+ *   d_B (num_cols x N fp16 bits) and d_C (num_rows x N fp32) 16-byte
  *   aligned, N % 8 == 0, N * 2 <= 16383; shape < 0 picks the default kernel
  *   shape (spmm_c_bsr_tile_shape lists them); the result equals spmm_c_wmma's
  *   within fp32 rounding (same products, same pairwise K order).

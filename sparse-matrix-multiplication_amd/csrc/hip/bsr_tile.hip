@@ -10,23 +10,29 @@
 // before it can address every A block and B row of its panel; the reference
 // kernel walks row_ptr and col_idx block by block.
 //
-// Workgroup = one panel x NT columns of C, four waves in a WR x WC grid (each
-// wave RW = R / WR block-rows x TC = NT / (16 WC) 16-column tiles).
-//   - The union's B rows (16 per slot, NT columns) are staged in LDS in chunks
-//     of CS slots with buffer-to-LDS loads (no VGPR staging), XOR-swizzled in
-//     16-byte units against bank conflicts, NB chunk buffers in a ring: NB - 1
-//     chunks are in flight while one is multiplied, one barrier per chunk.
-//   - Each wave loads the A operands of its own block-rows straight into
-//     VGPRs (structured-buffer records of one block), issued with the chunk.
-//   - Slots pair up as (2q, 2q+1): a block-row holding both multiplies them in
-//     one v_mfma_f32_16x16x32_f16; holding one of them (the ends of a run
-//     that starts or ends on an odd slot), in one v_mfma_f32_16x16x16_f16, so
-//     no matrix-core work is spent on absent blocks.  The B operand of a pair
-//     is read from LDS once per wave and feeds all of the wave's block-rows
-//     that hold the pair (register blocking over RW block-rows).
-//   - The MFMA operands are swapped (B^T as the M-side operand, A^T as the
-//     N-side one), so a lane's accumulators are four consecutive columns of
-//     one C row and C leaves in 16-byte stores straight from the registers.
+// Workgroup = one panel x NT columns of C; its multiplying waves form a
+// WR x WC grid (each wave RW = R / WR block-rows x TC = NT / (16 WC) 16-column
+// tiles).  Three forms share the plan, the B staging and the operand layouts
+// (the shape table in engine.h names the form as KIND):
+//   - producer / consumer (KIND 2, 3; the default): four waves only issue
+//     buffer-to-LDS loads of the panel's B rows (and, KIND 2, its A blocks)
+//     chunk by chunk, four waves only multiply; one barrier per chunk.  Each
+//     block-row's run is paired from its own first slot, (lo, lo+1), ..., in
+//     v_mfma_f32_16x16x32_f16, an odd last block in v_mfma_f32_16x16x16_f16,
+//     so the matrix cores multiply exactly the stored blocks.
+//   - one-shot and ring (KIND 1, 0): four waves that both load and multiply,
+//     A operands in VGPRs, the union's slots paired as (2q, 2q+1) with a
+//     16x16x16 MFMA for a run end on an odd slot; the ring (NB chunk buffers,
+//     NB - 1 chunks in flight) covers unions wider than the one-shot forms
+//     hold.
+//   - In all of them the union's B rows (16 per slot, NT columns) are staged
+//     with buffer-to-LDS loads (no VGPR staging), XOR-swizzled in 16-byte units
+//     against bank conflicts and read as MFMA operands with ds_read_b64_tr_b16;
+//     a pair's B operand is read once per wave for all of the wave's
+//     block-rows that hold it.  The operands are swapped (B^T as the M-side
+//     operand, A^T as the N-side one), so a lane's accumulators are four
+//     consecutive columns of one C row and C leaves in 16-byte stores straight
+//     from the registers.
 // Needs N % 8 == 0 with 16-byte aligned B and C, N * 2 <= 16383 bytes (the
 // record stride field) and A and B within 2 GiB each.
 
@@ -894,8 +900,12 @@ Error bsr_tile_plan_build(const BSR& d_A, int R, BsrTilePlan* out, hipStream_t s
     SPMM_TRY(bsr_tile_plan_from_host(rp.data(), ci.data(), d_A.block_rows, d_A.block_cols, R,
                                      &desc, &max_union));
     SPMM_TRY_HIP(hipMalloc(&out->desc, sizeof(int) * (desc.empty() ? 1 : desc.size())), "hipMalloc");
-    SPMM_TRY_HIP(hipMemcpy(out->desc, desc.data(), sizeof(int) * desc.size(), hipMemcpyHostToDevice),
-                 "hipMemcpy");
+    const hipError_t e =
+        hipMemcpy(out->desc, desc.data(), sizeof(int) * desc.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        bsr_tile_plan_free(out);
+        return hip_error(e, "hipMemcpy");
+    }
     out->R          = R;
     out->panels     = static_cast<int>(desc.size() / kTileDescInts);
     out->num_rows   = d_A.num_rows;
@@ -903,6 +913,8 @@ Error bsr_tile_plan_build(const BSR& d_A, int R, BsrTilePlan* out, hipStream_t s
     out->block_rows = d_A.block_rows;
     out->num_blocks = d_A.num_blocks;
     out->max_union  = max_union;
+    out->row_ptr    = d_A.row_ptr;
+    out->col_idx    = d_A.col_idx;
     return Error{};
 }
 
@@ -916,7 +928,8 @@ Error launch_bsr_tile(const BsrTilePlan& plan, const BSR& A, const half* B, floa
     if (N < 0) return fail(kInvalid, "negative matrix dimension");
     if (plan.desc == nullptr && plan.panels > 0) return fail(kInvalid, "empty plan");
     if (A.num_rows != plan.num_rows || A.num_cols != plan.num_cols ||
-        A.block_rows != plan.block_rows || A.num_blocks != plan.num_blocks) {
+        A.block_rows != plan.block_rows || A.num_blocks != plan.num_blocks ||
+        A.row_ptr != plan.row_ptr || A.col_idx != plan.col_idx) {
         return fail(kInvalid, "the plan was built for another matrix");
     }
     if (A.num_rows == 0 || N == 0) return Error{};

@@ -118,6 +118,8 @@ struct BsrTilePlan {
     int  block_rows = 0;
     int  num_blocks = 0;
     int  max_union  = 0;        // widest panel union, in block-columns
+    const int* row_ptr = nullptr;  // the structure arrays it was built from (checked at
+    const int* col_idx = nullptr;  // launch; the values may change between launches)
 };
 // Kernel shapes (id, R, NT columns per workgroup, WC wave columns, CS slots
 // per staged chunk, NB chunk buffers, KIND).  KIND 0: A operands in VGPRs, a

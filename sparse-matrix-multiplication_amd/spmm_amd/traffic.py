@@ -11,8 +11,9 @@ dispatched once per step (the merge-path forms have two: the engine and its
 fix-up), so set-up kernels dispatched once per run are left out.
 
 The JSON records the hash of the kernel sources that decide what the launch
-runs (`sources_sha256`); bench.py publishes the figure only while the current
-sources hash the same.
+runs (`sources_sha256`, over their code with comments and whitespace runs
+dropped); bench.py publishes the figure only while the current sources hash
+the same.
 
     python -m spmm_amd.traffic --cfg c2 --form engine --fetch D1 --write D2 \
         --copy-fetch D3 --copy-write D4 --commit <git sha> --out profiles/traffic_c2.json
@@ -23,6 +24,7 @@ import argparse
 import csv
 import glob
 import hashlib
+import re
 import json
 import os
 from collections import defaultdict
@@ -37,14 +39,23 @@ SOURCES = {
 }
 
 
+_COMMENT = re.compile(r"//[^\n]*|/\*.*?\*/", re.S)
+
+
+def code_text(src: str) -> str:
+    """The source without comments and with runs of whitespace collapsed: what
+    the compiler sees, so a comment edit does not void a capture."""
+    return " ".join(_COMMENT.sub(" ", src).split())
+
+
 def sources_sha256(backend: str) -> str:
     h = hashlib.sha256()
     for name in SOURCES[backend]:
         p = os.path.join(HIP_DIR, name)
         if os.path.exists(p):
             h.update(name.encode())
-            with open(p, "rb") as f:
-                h.update(f.read())
+            with open(p, encoding="utf-8") as f:
+                h.update(code_text(f.read()).encode())
     return h.hexdigest()
 
 

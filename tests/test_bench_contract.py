@@ -58,7 +58,7 @@ def test_stale_traffic_is_not_published(tmp_path, monkeypatch):
 
 
 def test_source_hash_follows_the_kernel_text(tmp_path, monkeypatch):
-    # the hash covers the kernel sources' names and bytes
+    # the hash covers the kernel sources' names and code
     hip = tmp_path / "hip"
     hip.mkdir()
     for n in traffic.SOURCES["csr"]:
@@ -67,6 +67,12 @@ def test_source_hash_follows_the_kernel_text(tmp_path, monkeypatch):
     h1 = traffic.sources_sha256("csr")
     (hip / traffic.SOURCES["csr"][0]).write_text("b")
     assert traffic.sources_sha256("csr") != h1
+    # comments and whitespace runs do not count; code does
+    h2 = traffic.sources_sha256("csr")
+    (hip / traffic.SOURCES["csr"][0]).write_text("b  // a note\n/* more */\n")
+    assert traffic.sources_sha256("csr") == h2
+    (hip / traffic.SOURCES["csr"][0]).write_text("b + 1")
+    assert traffic.sources_sha256("csr") != h2
 
 
 @pytest.mark.parametrize("backend", ["csr", "wmma"])

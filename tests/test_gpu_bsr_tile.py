@@ -187,6 +187,11 @@ def test_tile_refusals(S, O, torch):
     with pytest.raises(S.SpmmError) as e:
         plan.launch(torch.zeros((128, 16), dtype=torch.int16, device="cuda"))
     assert e.value.code == SPMM_INVALID
+    # the same matrix uploaded again: same sizes, other structure arrays -> refused
+    plan.A = S.DeviceBSR(hb)
+    with pytest.raises(S.SpmmError) as e:
+        plan.launch(torch.zeros((256, 16), dtype=torch.int16, device="cuda"))
+    assert e.value.code == SPMM_INVALID
 
 
 def test_tile_empty_matrix(S, O, torch):

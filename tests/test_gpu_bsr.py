@@ -136,7 +136,7 @@ def test_wmma_long_block_rows(S, O, torch):
     A.values = S.round_to_fp16(A.values)
     B = S.round_to_fp16(np.random.default_rng(3).uniform(-1, 1, (2048, 64)).astype(np.float32))
     hb, B16, C32, C64, absC = _refs(S, O, A, B)
-    assert np.diff(hb.row_ptr).max() > 126  # so every panel's union takes two passes
+    assert np.diff(hb.row_ptr).max() > 126  # so some panel's union takes two passes
     for rg, tiles, depth in ((4, 4, 2), (4, 8, 4), (8, 4, 4), (8, 8, 4), (1, 1, 0), (1, 2, 0),
                              (1, 4, 4)):
         say(f"wmma long block-rows row_group={rg} tiles={tiles} depth={depth} "

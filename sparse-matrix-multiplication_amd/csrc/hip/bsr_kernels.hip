@@ -20,32 +20,18 @@
 #include <initializer_list>
 #include <type_traits>
 
+#include "amdgcn.h"
 #include "engine.h"
 #include "spmm/utils.h"
-
-typedef unsigned spmm_u32x4 __attribute__((ext_vector_type(4)));
-
-// Structured buffer load (LLVM's AMDGPU intrinsic; index = record, offset =
-// byte offset inside the record).  The intrinsic name is fixed by LLVM.
-__device__ spmm_u32x4 sbuf_load_u32x4(__amdgpu_buffer_rsrc_t rsrc, int index, int offset,
-                                      int soffset, int aux)
-    __asm("llvm.amdgcn.struct.ptr.buffer.load.v4i32");
-// Structured buffer load straight into LDS: every lane's `size` bytes land at
-// the LDS address p + 16 * lane (gfx950 LDS DMA), nothing passes through VGPRs.
-typedef __attribute__((address_space(3))) void* spmm_lds_ptr;
-__device__ void sbuf_load_lds(__amdgpu_buffer_rsrc_t rsrc, spmm_lds_ptr p, int size, int index,
-                              int offset, int soffset, int imm_offset, int aux)
-    __asm("llvm.amdgcn.struct.ptr.buffer.load.lds");
 
 namespace spmm {
 namespace engine {
 
 namespace {
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+using namespace dev;  // vector types, buffer loads, waits, barriers (amdgcn.h)
+
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef float    f32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // fp32 -> fp16 (round to nearest even), 8 elements per lane on the aligned body.
 __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict__ src,
@@ -79,13 +65,11 @@ __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict
 // it from displacing A and B in L2 (measured on c4: 7.8 -> 7.5 us).
 __device__ __forceinline__ void store_c(float* p, float v) { __builtin_nontemporal_store(v, p); }
 
-// Cache policy of the record kernel's 16-byte C row chunks: device scope (the
-// sc1 bit of a buffer instruction's policy operand).  Measured on MI355X
-// against streaming stores of the same chunks (A/B over three rounds, results
-// bit-identical): c3 3.84 -> 3.65 us, c4 5.88 -> 5.79 us per launch.  The CSR
-// kernels measured slower with it (c1 +7%, c2 +1.5%, c5 +2-3%) and keep
-// streaming stores.
-constexpr int kStoreDevice = 16;
+// The record kernel stores its 16-byte C row chunks with device scope
+// (kStoreDevice, the sc1 bit).  Measured on MI355X against streaming stores of
+// the same chunks (A/B over three rounds, results bit-identical): c3 3.84 ->
+// 3.65 us, c4 5.88 -> 5.79 us per launch.  The CSR kernels measured slower
+// with it (c1 +7%, c2 +1.5%, c5 +2-3%) and keep streaming stores.
 
 struct BsrArgs {
     const int*      row_ptr;
@@ -124,19 +108,6 @@ __device__ __forceinline__ void wave_tile_of(const BsrArgs& a, int& bx, int& by)
     by = l - bx * a.tiles_n;
 }
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef short s16x8 __attribute__((ext_vector_type(8)));
-
-// ds_read_b64_tr_b16.  Within each 16-lane block, lane s supplies the address
-// of 4 consecutive fp16 values and output lane i receives element i % 4 of
-// the values addressed by lanes 4e + i/4, e = 0..3: with lane s pointing at
-// row s/4, columns 4*(s%4) .. +3 of a row-major [k][n] tile, lane i gets
-// rows 0..3 of column i -- a K-contiguous MFMA B operand.
-__device__ __forceinline__ s16x4 lds_read_tr16(const _Float16* p) {
-    // generic -> LDS address-space cast; p always points into a __shared__ array
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) s16x4*)(const_cast<_Float16*>(p)));
-}
 
 // ---------------------------------------------------------------------------
 // Wave kernel (the default path): one wave = one block-row x 16*J columns,
@@ -309,26 +280,6 @@ __global__ __launch_bounds__(256) void bsr_wave_kernel(BsrArgs a) {
 // ---------------------------------------------------------------------------
 __device__ u32x4 sbuf_load_u32x4_dev(__amdgpu_buffer_rsrc_t rsrc, int index, int offset) {
     return sbuf_load_u32x4(rsrc, index, offset, 0, 0);
-}
-
-// Third dword of a gfx9 buffer resource: 32-bit data format, no swizzle.
-constexpr int kBufWord3 = 0x00020000;
-
-// s_waitcnt constraining only the vector-memory count (gfx9 encoding:
-// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).
-template <int VM>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(VM >= 0 && VM < 64, "vmcnt is 6 bits");
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt((VM & 0xF) | ((VM >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-// Workgroup barrier without a memory fence: the caller has already waited
-// for the LDS writes (and buffer-to-LDS loads) its partners must see.  The
-// memory clobber keeps the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 template <int J, int D>

@@ -9,7 +9,9 @@ C(A, B1 + B2) = C(A, B1) + C(A, B2) up to fp32 rounding.
 * 131 072 x 2 560 000 CSR with N = 256: B of 2.6 GB, past the 2 GiB a
   structured buffer can address, so the engine falls back to 64-bit address
   loads.
-* banded 262 144^2 (half-bandwidth 32) on the MFMA path with N = 128.
+* banded 262 144^2 (half-bandwidth 32) on the MFMA path with N = 128, and the
+  run-panel form on it and on block-diagonal 262 144^2 (1024 blocks of 256^2)
+  at N = 256.
 * 262 144 x 16 384 power-law rows (mean 164, capped at 4096; ~43 M nonzeros) with N = 128:
   B of 8 MiB, so the hybrid's form is merge-path over B-row halves.
 """
@@ -122,6 +124,51 @@ def test_large_mfma(S, O, torch):
     check_bsr(got, ref, absr)
     check_csr(got, ref, absr, tol=1e-5)  # fp16 products are exact in fp32
     assert not torch.isnan(C).any().item()
+
+
+@pytest.mark.parametrize("kind", ["band", "diag"])
+def test_large_tile(S, O, torch, kind):
+    # The run-panel form at 262144 rows (the hybrid's MFMA form on structured
+    # input): sampled rows against fp64, every row written, and whole-output
+    # sign symmetry (within rounding) and determinism through the same plan.
+    M = 262144
+    if kind == "band":
+        A, N = S.generate_banded_csr(M, M, 32, 76), 128
+    else:
+        A, N = S.generate_block_diagonal_csr(M, M, 256, 77, 0.1), 256
+    A.values = S.round_to_fp16(A.values)
+    rng = np.random.default_rng(78)
+    B = S.round_to_fp16(rng.uniform(-1, 1, size=(M, N)).astype(np.float32))
+    hb = S.bsr_from_csr_host(A)
+    dA = S.DeviceBSR(hb)
+    plan = S.BsrTilePlan(dA)
+    say(f"large tile {kind} M={M} nnz={A.nnz} blocks={hb.num_blocks} N={N} "
+        f"panels={plan.panels} max_union={plan.max_union} shape={plan.default_shape(N)}")
+    B16 = O.f32_to_f16(B)
+    dB = torch.from_numpy(B16.view(np.int16)).cuda()
+    C1 = torch.full((M, N), float("nan"), device="cuda")
+    plan.launch(dB, C1)
+    torch.cuda.synchronize()
+    assert not torch.isnan(C1).any().item(), "every row of C is written"
+    rows = np.sort(rng.choice(M, size=2000, replace=False))
+    Bh = B16.view(np.float16).astype(np.float32)
+    ref, absr = _sample_ref(A, Bh, rows)
+    got = C1[torch.from_numpy(rows).cuda()].cpu().numpy()
+    check_bsr(got, ref, absr)
+    check_csr(got, ref, absr, tol=1e-5)  # fp16 products are exact in fp32
+    # whole output: C(A, -B) = -C(A, B) within fp32 rounding (the matrix cores'
+    # internal accumulation is not sign-symmetric to the last bit), and a
+    # second launch reproduces C bit for bit
+    Cneg = plan.launch((-dB.view(torch.float16)).contiguous().view(torch.int16))
+    Cagain = plan.launch(dB)
+    torch.cuda.synchronize()
+    asym = (Cneg + C1).abs()
+    say(f"large tile {kind}: C(-B) + C(B) max {asym.max().item():.3e} over "
+        f"{int((asym > 0).sum().item())} of {asym.numel()} elements; max |C| "
+        f"{C1.abs().max().item():.3f}")
+    assert asym.max().item() <= 1e-5 * C1.abs().max().item()
+    assert torch.equal(Cagain, C1)
+    plan.close()
 
 
 def test_large_khalf(S, torch):

@@ -6,9 +6,9 @@
 //
 // A timing diagnostic, no counterpart in the reference.  On MI355X the DPM
 // state reads its top level (2.4 GHz) from the first launch, yet under the
-// full load of the SpMM kernels the delivered clock starts near 2.1 GHz after
-// an idle period and rises to about 2.38 GHz over roughly a thousand
-// back-to-back launches; a lone sampler on an idle GPU reads about 2.4 GHz.
+// full load of the SpMM kernels the delivered clock starts near 2.15 GHz
+// after an idle period and rises to about 2.39 GHz over some 600 back-to-back
+// launches; a lone sampler on an idle GPU reads about 2.4 GHz.
 //
 // The wave only sleeps between samples and ends after samples x interval
 // ticks of real time (bounded by the launcher), whatever else runs.

@@ -44,6 +44,14 @@ Error run_unified(const CSR& h_A, const float* h_B, float* h_C, int N, int warmu
     const int M = h_A.num_rows;
     const int K = h_A.num_cols;
     if (M < 0 || K < 0 || N < 0 || h_A.nnz < 0) return Error{kInvalid, "negative dimension"};
+    // Host arrays are read (and C written) before any launch: refuse missing
+    // ones here rather than fault in the copies.
+    if (h_A.row_ptr == nullptr ||
+        (h_A.nnz > 0 && (h_A.col_idx == nullptr || h_A.values == nullptr)) ||
+        (static_cast<size_t>(K) * N > 0 && h_B == nullptr) ||
+        (static_cast<size_t>(M) * N > 0 && h_C == nullptr)) {
+        return Error{kInvalid, "null host array"};
+    }
     int dev = 0;
     SPMM_TRY_HIP(hipGetDevice(&dev), "hipGetDevice");
     int managed = 0;

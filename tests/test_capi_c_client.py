@@ -2,8 +2,9 @@
 with gcc against include/spmm_capi.h and linked to libspmm_amd.so, calling
 host-side entry points — the reference's uniform generator (csr.cu:74-103;
 its committed nnz for 4096^2, density 0.01, seed 42 is 167686), the hybrid
-rule (spmm_hybrid.cu:32-56), the host free that zeroes the struct, and an
-error that comes back as a status with a message instead of exiting."""
+rule (spmm_hybrid.cu:32-56), the host free that zeroes the struct, an error
+that comes back as a status with a message instead of exiting, and
+spmm_c_unified refusing a matrix without row_ptr before any device call."""
 import os
 import shutil
 import subprocess
@@ -40,6 +41,17 @@ int main(void) {
     const int bad_rc = spmm_c_generate_uniform_random_csr(-1, 4, 0.5f, 1, &bad);
     printf("bad_rc=%d message=%d version=%d\n", bad_rc, spmm_c_last_error()[0] != '\0',
            spmm_c_version()[0] != '\0');
+    /* spmm_unified with a missing row_ptr: refused before any device call */
+    spmm_csr_t hole;
+    memset(&hole, 0, sizeof hole);
+    hole.num_rows = 4;
+    hole.num_cols = 4;
+    float b[16] = {0}, c[16];
+    float ms = -1.0f;
+    int residency = 7;
+    const int un_rc = spmm_c_unified(&hole, b, c, 4, 0, 1, &ms, &residency);
+    printf("unified_rc=%d invalid=%d untouched=%d\n", un_rc, un_rc == SPMM_INVALID,
+           ms == -1.0f && residency == 7);
     return 0;
 }
 """
@@ -66,3 +78,5 @@ def test_c11_client_links_and_runs(S, tmp_path):
     assert lines[1] == "freed rows=0 nnz=0 null=1"
     bad = dict(kv.split("=") for kv in lines[2].split())
     assert bad["bad_rc"] != "0" and bad["message"] == "1" and bad["version"] == "1"
+    unified = dict(kv.split("=") for kv in lines[3].split())
+    assert unified["invalid"] == "1" and unified["untouched"] == "1", lines[3]

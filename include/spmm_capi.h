@@ -331,7 +331,10 @@ int  spmm_c_bsr_tile_default_shape(const spmm_bsr_tile_plan_t* plan, int N);
  * counterpart in the reference (its default is the constant 2.0). */
 float spmm_c_hybrid_default_threshold(void);
 float spmm_c_hybrid_default_threshold_for(int N);
-/* fill_in_threshold < 0 selects spmm_c_hybrid_default_threshold_for(N). */
+/* fill_in_threshold < 0 selects spmm_c_hybrid_default_threshold_for(N).
+ * The host-in calls (choose, run, unified) return SPMM_INVALID for a host CSR
+ * with negative sizes, no row_ptr, or entries without col_idx (or, to run,
+ * without values), before reading it or touching the device. */
 int spmm_c_hybrid_choose(const spmm_csr_t* h_A, int N, float fill_in_threshold,
                          spmm_hybrid_plan_t* out);               /* spmm_hybrid.h:48 */
 const char* spmm_c_backend_name(int backend);                    /* spmm_hybrid.h:51 */

@@ -821,11 +821,22 @@ int spmm_c_launch_repeat_wmma_opts(const spmm_bsr_t* d_bsr, const uint16_t* d_B1
 
 // ---- hybrid ------------------------------------------------------------------
 
+namespace {
+// A host CSR whose arrays the host-in entry points may read: non-negative
+// sizes, row_ptr present, and (with entries) col_idx, plus values when the
+// numbers are used.  The C++ API trusts its caller as the reference does.
+bool host_csr_ok(const spmm_csr_t& h, bool values) {
+    return h.num_rows >= 0 && h.num_cols >= 0 && h.nnz >= 0 && h.row_ptr != nullptr &&
+           (h.nnz == 0 || (h.col_idx != nullptr && (!values || h.values != nullptr)));
+}
+}  // namespace
+
 float spmm_c_hybrid_default_threshold(void) { return spmm::kHybridDefaultThreshold; }
 float spmm_c_hybrid_default_threshold_for(int N) { return spmm::hybrid_default_threshold(N); }
 
 int spmm_c_hybrid_choose(const spmm_csr_t* h_A, int N, float thr, spmm_hybrid_plan_t* out) {
     if (h_A == nullptr || out == nullptr) return set_error(SPMM_INVALID, "null argument");
+    if (!host_csr_ok(*h_A, false)) return set_error(SPMM_INVALID, "bad host CSR");
     return guarded([&] {
         const spmm::HybridPlan p = spmm::hybrid_choose(to_cpp(*h_A), N, thr);
         out->backend       = p.backend == spmm::Backend::TENSOR_WMMA ? SPMM_BACKEND_WMMA
@@ -849,6 +860,10 @@ int spmm_c_hybrid_run(const spmm_hybrid_plan_t* plan, const spmm_csr_t* h_A, con
     if (plan == nullptr || h_A == nullptr || h_C == nullptr || N < 0 || warmup < 0 ||
         iters < 0) {
         return set_error(SPMM_INVALID, "bad argument");
+    }
+    if (!host_csr_ok(*h_A, true)) return set_error(SPMM_INVALID, "bad host CSR");
+    if (h_B == nullptr && static_cast<long>(h_A->num_cols) * N > 0) {
+        return set_error(SPMM_INVALID, "null B");
     }
     return guarded([&] {
         spmm::HybridPlan p;
@@ -877,6 +892,7 @@ int spmm_c_unified(const spmm_csr_t* h_A, const float* h_B, float* h_C, int N, i
     if (h_A == nullptr || h_C == nullptr || N < 0 || warmup < 0 || iters < 0) {
         return set_error(SPMM_INVALID, "bad argument");
     }
+    if (!host_csr_ok(*h_A, true)) return set_error(SPMM_INVALID, "bad host CSR");
     if (h_B == nullptr && static_cast<long>(h_A->num_cols) * N > 0) {
         return set_error(SPMM_INVALID, "null B");
     }

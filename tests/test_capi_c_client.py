@@ -4,7 +4,8 @@ host-side entry points — the reference's uniform generator (csr.cu:74-103;
 its committed nnz for 4096^2, density 0.01, seed 42 is 167686), the hybrid
 rule (spmm_hybrid.cu:32-56), the host free that zeroes the struct, an error
 that comes back as a status with a message instead of exiting, and
-spmm_c_unified refusing a matrix without row_ptr before any device call."""
+spmm_c_unified, spmm_c_hybrid_choose and spmm_c_hybrid_run refusing a matrix
+without row_ptr before reading it or calling the device."""
 import os
 import shutil
 import subprocess
@@ -52,6 +53,14 @@ int main(void) {
     const int un_rc = spmm_c_unified(&hole, b, c, 4, 0, 1, &ms, &residency);
     printf("unified_rc=%d invalid=%d untouched=%d\n", un_rc, un_rc == SPMM_INVALID,
            ms == -1.0f && residency == 7);
+    /* the same matrix through the hybrid's choice and run */
+    spmm_hybrid_plan_t hp;
+    memset(&hp, 0, sizeof hp);
+    const int ch_rc = spmm_c_hybrid_choose(&hole, 4, -1.0f, &hp);
+    hp.backend = SPMM_BACKEND_CSR;
+    const int hy_rc = spmm_c_hybrid_run(&hp, &hole, b, c, 4, 0, 1, &ms);
+    printf("choose_invalid=%d run_invalid=%d untouched=%d\n", ch_rc == SPMM_INVALID,
+           hy_rc == SPMM_INVALID, ms == -1.0f);
     return 0;
 }
 """
@@ -80,3 +89,4 @@ def test_c11_client_links_and_runs(S, tmp_path):
     assert bad["bad_rc"] != "0" and bad["message"] == "1" and bad["version"] == "1"
     unified = dict(kv.split("=") for kv in lines[3].split())
     assert unified["invalid"] == "1" and unified["untouched"] == "1", lines[3]
+    assert lines[4] == "choose_invalid=1 run_invalid=1 untouched=1", lines[4]

@@ -121,12 +121,13 @@ def test_tile_full_configs(S, O, torch, name):
         check_csr(C, C64, absC, tol=1e-5)
 
 
-def test_tile_fuzz(S, O, torch):
+@pytest.mark.parametrize("seed", [77, 78, 79])
+def test_tile_fuzz(S, O, torch, seed):
     # Seeded random run structures (tile_cases.random_case: random run starts
     # and lengths, empty block-rows, ragged M and K) at random N (multiples of 8),
     # every kernel shape whose union fits, R = 4 and 8, against the oracle.
     from tile_cases import random_case, panels_contiguous
-    rng = np.random.default_rng(77)
+    rng = np.random.default_rng(seed)
     shapes = S.bsr_tile_shapes()
     done = 0
     while done < 24:

@@ -64,7 +64,7 @@ def _shape(rng):
     return M, K, N
 
 
-@pytest.mark.parametrize("chunk", range(4))
+@pytest.mark.parametrize("chunk", range(10))
 def test_csr_engine_random(S, O, torch, chunk):
     rng = np.random.default_rng(1000 + chunk)
     hint_rng = np.random.default_rng(5000 + chunk)
@@ -107,7 +107,7 @@ def test_csr_engine_random(S, O, torch, chunk):
             check_csr(dC.cpu().numpy(), C64, absC)
 
 
-@pytest.mark.parametrize("chunk", range(3))
+@pytest.mark.parametrize("chunk", range(10))
 def test_mfma_random(S, O, torch, chunk):
     rng = np.random.default_rng(2000 + chunk)
     for case in range(25):
@@ -160,7 +160,7 @@ def _long_row_csr(S, rng, M, K):
     return S.csr_from_coo_host(M, K, r, c, rng.uniform(-1, 1, r.size).astype(np.float32))
 
 
-@pytest.mark.parametrize("chunk", range(2))
+@pytest.mark.parametrize("chunk", range(5))
 def test_row_groups_random(S, O, torch, chunk):
     # the sub-wave row groups under random shapes, skew, load forms, column
     # slices, entry lanes, unroll and longest-row hints (exact, above, and
@@ -214,7 +214,7 @@ def _halves_csr(S, rng, M, K):
     return S.HostCSR(M, K, row_ptr, col, rng.uniform(-1, 1, col.size).astype(np.float32))
 
 
-@pytest.mark.parametrize("chunk", range(2))
+@pytest.mark.parametrize("chunk", range(4))
 def test_khalf_random(S, O, torch, chunk):
     # merge-path over B-row halves on random shapes that qualify (N % 4 == 0,
     # K x N x 4 bytes over 4 MiB with half of the rows within it); a plan with
